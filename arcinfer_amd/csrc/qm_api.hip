@@ -1,0 +1,435 @@
+// The C ABI of include/qmatmul.h: argument and shape checks, weight preparation, workspace layout, launches.
+// Never throws or exits; errors come back as qm_status with a message in qmatmul_last_error().
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/qmatmul.h"
+#include "qm_launch.h"
+
+struct qm_weight {
+  int type, rows, K, device;
+  uint8_t* base;
+  size_t bytes;
+  qm::WView view;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(QM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool known_type(int t) { return t == QM_Q8_0 || t == QM_Q4_K || t == QM_IQ3_S || t == QM_IQ4_XS; }
+
+int payload_bytes(int t) { return t == QM_Q8_0 ? 32 : t == QM_IQ3_S ? 12 : 16; }
+int header_bytes(int t) { return t == QM_IQ4_XS ? 8 : 16; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t plane_qs_bytes(int t, int rows, int K) { return (size_t)rows * (K / 32) * payload_bytes(t); }
+size_t plane_hdr_bytes(int t, int rows, int K) { return (size_t)rows * (K / 256) * header_bytes(t); }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+std::once_flag g_init_once;
+int g_init_status = QM_OK;
+char g_init_err[512] = "";
+
+int ensure_init() {
+  std::call_once(g_init_once, [] {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    hipDeviceProp_t p;
+    if (e == hipSuccess) e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) {
+      g_init_status = QM_ERR_HIP;
+      snprintf(g_init_err, sizeof(g_init_err), "qmatmul_init: %s", hipGetErrorString(e));
+      return;
+    }
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+      g_init_status = QM_ERR_HIP;
+      snprintf(g_init_err, sizeof(g_init_err), "qmatmul_init: device is %s, the kernels are built for gfx950",
+               p.gcnArchName);
+    }
+  });
+  if (g_init_status != QM_OK) return fail(g_init_status, "%s", g_init_err);
+  return QM_OK;
+}
+
+#define QM_CHECK_INIT()            \
+  do {                             \
+    const int st_ = ensure_init(); \
+    if (st_) return st_;           \
+  } while (0)
+
+struct MoeLayout {
+  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, total;
+  int slots, max_tiles, tile_rows;
+};
+
+constexpr int kMoeTileRows = 32;
+
+MoeLayout moe_layout(int T, int NE, int NU, int E, int F) {
+  MoeLayout L;
+  L.slots = T * NU;
+  L.tile_rows = kMoeTileRows;
+  L.max_tiles = (L.slots + kMoeTileRows - 1) / kMoeTileRows + NE;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  L.ids = take(sizeof(int) * (size_t)L.slots);
+  L.wts = take(sizeof(float) * (size_t)L.slots);
+  L.counts = take(sizeof(int) * (size_t)NE);
+  L.cursor = take(sizeof(int) * (size_t)NE);
+  L.tstart = take(sizeof(int) * (size_t)(NE + 1));
+  L.tiles = take(sizeof(int) * (size_t)(1 + 3 * L.max_tiles));
+  L.stok = take(sizeof(int) * (size_t)L.slots);
+  L.swt = take(sizeof(float) * (size_t)L.slots);
+  L.inv = take(sizeof(int) * (size_t)L.slots);
+  L.hq = take((size_t)L.slots * F);
+  L.hsc = take(sizeof(float) * (size_t)(F / 32) * L.slots);
+  L.y = take(sizeof(float) * (size_t)L.slots * E);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmatmul_init(void) {
+  QM_CHECK_INIT();
+  return QM_OK;
+}
+
+const char* qmatmul_last_error(void) { return g_err; }
+
+size_t qmatmul_sb_bytes(int type) {
+  switch (type) {
+    case QM_Q8_0: return 272;
+    case QM_Q4_K: return 144;
+    case QM_IQ3_S: return 110;
+    case QM_IQ4_XS: return 136;
+    default: return 0;
+  }
+}
+
+size_t qmatmul_weight_bytes(int type, int rows, int K) {
+  if (!known_type(type) || rows <= 0 || K <= 0 || K % 256) return 0;
+  return align256(plane_qs_bytes(type, rows, K)) + plane_hdr_bytes(type, rows, K);
+}
+
+int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int rows, int K, void* stream,
+                           qm_weight** out) {
+  if (!out || !raw) return fail(QM_ERR_ARG, "qmatmul_prepare_weight: null pointer");
+  *out = nullptr;
+  if (!known_type(type)) return fail(QM_ERR_TYPE, "qmatmul_prepare_weight: unsupported type %d", type);
+  if (rows <= 0 || K <= 0 || K % 256)
+    return fail(QM_ERR_SHAPE, "qmatmul_prepare_weight: rows %d, K %d (K must be a positive multiple of 256)", rows, K);
+  QM_CHECK_INIT();
+  hipStream_t s = (hipStream_t)stream;
+  const size_t qsb = plane_qs_bytes(type, rows, K), total = qmatmul_weight_bytes(type, rows, K);
+  const size_t rawb = (size_t)rows * (K / 256) * qmatmul_sb_bytes(type);
+  qm_weight* w = new (std::nothrow) qm_weight();
+  if (!w) return fail(QM_ERR_NOMEM, "qmatmul_prepare_weight: host allocation");
+  hipError_t e = hipGetDevice(&w->device);
+  if (e != hipSuccess) {
+    delete w;
+    return hip_fail(e, "qmatmul_prepare_weight: hipGetDevice");
+  }
+  e = hipMalloc((void**)&w->base, total);
+  if (e != hipSuccess) {
+    delete w;
+    return fail(QM_ERR_NOMEM, "qmatmul_prepare_weight: hipMalloc(%zu): %s", total, hipGetErrorString(e));
+  }
+  const uint8_t* src = (const uint8_t*)raw;
+  uint8_t* staged = nullptr;
+  if (!raw_on_device) {
+    e = hipMalloc((void**)&staged, rawb);
+    if (e == hipSuccess) e = hipMemcpyAsync(staged, raw, rawb, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) {
+      if (staged) (void)hipFree(staged);
+      (void)hipFree(w->base);
+      delete w;
+      return hip_fail(e, "qmatmul_prepare_weight: staging the host bytes");
+    }
+    src = staged;
+  }
+  w->type = type;
+  w->rows = rows;
+  w->K = K;
+  w->bytes = total;
+  w->view.qs = w->base;
+  w->view.hdr = w->base + align256(qsb);
+  w->view.rows = rows;
+  w->view.K = K;
+  e = qm::launch_repack(type, src, rows, K, w->base, w->base + align256(qsb), s);
+  if (e == hipSuccess && staged) e = hipStreamSynchronize(s);
+  if (staged) (void)hipFree(staged);
+  if (e != hipSuccess) {
+    (void)hipFree(w->base);
+    delete w;
+    return hip_fail(e, "qmatmul_prepare_weight: repack");
+  }
+  *out = w;
+  return QM_OK;
+}
+
+int qmatmul_release_weight(qm_weight* w) {
+  if (!w) return fail(QM_ERR_ARG, "qmatmul_release_weight: null weight");
+  hipError_t e = hipFree(w->base);
+  delete w;
+  if (e != hipSuccess) return hip_fail(e, "qmatmul_release_weight: hipFree");
+  return QM_OK;
+}
+
+int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K) {
+  if (!w) return fail(QM_ERR_ARG, "qmatmul_weight_info: null weight");
+  if (type) *type = w->type;
+  if (rows) *rows = w->rows;
+  if (K) *K = w->K;
+  return QM_OK;
+}
+
+int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
+                         void* stream) {
+  if (!x || !aq || !asc || !absum) return fail(QM_ERR_ARG, "qmatmul_quantize_act: null pointer");
+  if (K <= 0 || K % 32 || M < 0 || M_stride < 1 || M > M_stride || ldx < K)
+    return fail(QM_ERR_SHAPE, "qmatmul_quantize_act: M %d, M_stride %d, K %d, ldx %d", M, M_stride, K, ldx);
+  if (!aligned(aq, 4)) return fail(QM_ERR_ARG, "qmatmul_quantize_act: aq must be 4-byte aligned");
+  QM_CHECK_INIT();
+  const hipError_t e = qm::launch_quantize(x, ldx, M, M_stride, K, aq, asc, absum, (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_quantize_act");
+}
+
+static int check_acts(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
+                      int rows_needed, int M_stride) {
+  if (!w || !aq || !asc) return fail(QM_ERR_ARG, "%s: null pointer", fn);
+  if (w->type == QM_Q4_K && !absum) return fail(QM_ERR_ARG, "%s: Q4_K needs the per-16 activation sums", fn);
+  if (rows_needed < 1 || M_stride < rows_needed)
+    return fail(QM_ERR_SHAPE, "%s: %d activation rows with M_stride %d", fn, rows_needed, M_stride);
+  if (!aligned(aq, 16)) return fail(QM_ERR_ARG, "%s: aq must be 16-byte aligned", fn);
+  return QM_OK;
+}
+
+int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,
+                 float* C, int ldc, int c_off, int accumulate, void* stream) {
+  if (int st = check_acts("qmatmul_gemv", w, aq, asc, absum, T, M_stride)) return st;
+  if (!C) return fail(QM_ERR_ARG, "qmatmul_gemv: null output");
+  if (T < 1 || T > 8) return fail(QM_ERR_SHAPE, "qmatmul_gemv: T = %d (1..8 tokens per call)", T);
+  if (accumulate != 0 && accumulate != 1) return fail(QM_ERR_ARG, "qmatmul_gemv: accumulate %d (0 or 1)", accumulate);
+  if (c_off < 0 || (T > 1 && ldc < c_off + w->rows))
+    return fail(QM_ERR_SHAPE, "qmatmul_gemv: ldc %d, c_off %d, rows %d", ldc, c_off, w->rows);
+  QM_CHECK_INIT();
+  qm::GemvArgs a{};
+  a.w = w->view;
+  a.aq = aq;
+  a.asc = asc;
+  a.absum = absum;
+  a.M_stride = M_stride;
+  a.T = T;
+  a.C = C;
+  a.ldc = ldc;
+  a.c_off = c_off;
+  a.accumulate = accumulate;
+  const hipError_t e = qm::launch_gemv(w->type, a, (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemv");
+}
+
+int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* absum, int M_stride, int T,
+                           int32_t* isum, int32_t* msum, void* stream) {
+  static const float unused = 0.0f;  // (the block-sum mode reads no scales)
+  if (int st = check_acts("qmatmul_gemv_blocksums", w, aq, &unused, absum, T, M_stride)) return st;
+  if (!isum || (w->type == QM_Q4_K && !msum)) return fail(QM_ERR_ARG, "qmatmul_gemv_blocksums: null output");
+  if (T < 1 || T > 8) return fail(QM_ERR_SHAPE, "qmatmul_gemv_blocksums: T = %d", T);
+  QM_CHECK_INIT();
+  qm::GemvArgs a{};
+  a.w = w->view;
+  a.aq = aq;
+  a.absum = absum;
+  a.M_stride = M_stride;
+  a.T = T;
+  a.dbg_isum = isum;
+  a.dbg_msum = msum;
+  const hipError_t e = qm::launch_gemv(w->type, a, (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemv_blocksums");
+}
+
+int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                 float* C, int ldc, int c_off, int accumulate, void* stream) {
+  if (int st = check_acts("qmatmul_gemm", w, aq, asc, absum, M, M_stride)) return st;
+  if (!C) return fail(QM_ERR_ARG, "qmatmul_gemm: null output");
+  if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm: rows %d not a multiple of 16", w->rows);
+  if (accumulate < 0 || accumulate > 2) return fail(QM_ERR_ARG, "qmatmul_gemm: accumulate %d (0..2)", accumulate);
+  if (c_off < 0 || ldc < c_off + w->rows)
+    return fail(QM_ERR_SHAPE, "qmatmul_gemm: ldc %d, c_off %d, rows %d", ldc, c_off, w->rows);
+  QM_CHECK_INIT();
+  qm::GemmArgs a{};
+  a.w = w->view;
+  a.aq = aq;
+  a.asc = asc;
+  a.absum = absum;
+  a.M = M;
+  a.M_stride = M_stride;
+  a.C = C;
+  a.ldc = ldc;
+  a.c_off = c_off;
+  a.accumulate = accumulate;
+  const hipError_t e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm");
+}
+
+int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream) {
+  static const float unused = 0.0f;  // (the block-sum mode reads no scales or sums)
+  if (int st = check_acts("qmatmul_gemm_blocksums", w, aq, &unused, (const int16_t*)&unused, M, M_stride)) return st;
+  if (!isum) return fail(QM_ERR_ARG, "qmatmul_gemm_blocksums: null output");
+  if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm_blocksums: rows %d not a multiple of 16", w->rows);
+  QM_CHECK_INIT();
+  qm::GemmArgs a{};
+  a.w = w->view;
+  a.aq = aq;
+  a.M = M;
+  a.M_stride = M_stride;
+  a.dbg_isum = isum;
+  const hipError_t e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm_blocksums");
+}
+
+size_t qmatmul_moe_workspace_size(int T, int NE, int NU, int E, int F) {
+  if (T < 1 || NE < 1 || NU < 1 || E < 1 || F < 1) return 0;
+  return moe_layout(T, NE, NU, E, F).total;
+}
+
+int qmatmul_moe_ws_layout(int T, int NE, int NU, int E, int F, qm_moe_ws_layout* out) {
+  if (!out) return fail(QM_ERR_ARG, "qmatmul_moe_ws_layout: null output");
+  if (T < 1 || NE < 1 || NU < 1 || E < 1 || F < 1) return fail(QM_ERR_SHAPE, "qmatmul_moe_ws_layout: bad sizes");
+  const MoeLayout L = moe_layout(T, NE, NU, E, F);
+  out->ids = L.ids;
+  out->wts = L.wts;
+  out->counts = L.counts;
+  out->cursor = L.cursor;
+  out->tstart = L.tstart;
+  out->tiles = L.tiles;
+  out->stok = L.stok;
+  out->swt = L.swt;
+  out->inv = L.inv;
+  out->hq = L.hq;
+  out->hsc = L.hsc;
+  out->y = L.y;
+  out->total = L.total;
+  out->slots = L.slots;
+  out->max_tiles = L.max_tiles;
+  out->tile_rows = L.tile_rows;
+  return QM_OK;
+}
+
+int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
+                      void* stream) {
+  if (!logits || !ids || !wts) return fail(QM_ERR_ARG, "qmatmul_moe_route: null pointer");
+  if (T < 1 || NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || ldl < NE)
+    return fail(QM_ERR_SHAPE, "qmatmul_moe_route: T %d, NE %d (<= 1024), NU %d (<= 64), ldl %d", T, NE, NU, ldl);
+  QM_CHECK_INIT();
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (counts) e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
+  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_route");
+}
+
+int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
+                        int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,
+                        int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
+    return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
+  for (const qm_weight* w : {gate, up, down})
+    if (w->type == QM_Q4_K)
+      return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: expert weights with per-block mins (Q4_K) are not supported");
+  if (gate->type != up->type)
+    return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: gate and up must have one type (got %d, %d)", gate->type, up->type);
+  if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)
+    return fail(QM_ERR_SHAPE, "qmatmul_moe_grouped: NE %d, NU %d, T %d, M_stride %d, ldl %d", NE, NU, T, M_stride, ldl);
+  const int E = gate->K, F = down->K;
+  if (gate->rows != NE * F || up->rows != NE * F || up->K != E || down->rows != NE * E || F % 32 || E % 4)
+    return fail(QM_ERR_SHAPE,
+                "qmatmul_moe_grouped: gate %dx%d, up %dx%d, down %dx%d do not fit NE %d experts of F x E / E x F",
+                gate->rows, gate->K, up->rows, up->K, down->rows, down->K, NE);
+  if (accumulate != 0 && accumulate != 1)
+    return fail(QM_ERR_ARG, "qmatmul_moe_grouped: accumulate %d (0 or 1)", accumulate);
+  if (!aligned(aq, 16) || !aligned(x, 16) || !aligned(ws, 256))
+    return fail(QM_ERR_ARG, "qmatmul_moe_grouped: aq/x need 16-byte, ws 256-byte alignment");
+  const MoeLayout L = moe_layout(T, NE, NU, E, F);
+  if (ws_bytes < L.total)
+    return fail(QM_ERR_WORKSPACE, "qmatmul_moe_grouped: workspace %zu < %zu bytes", ws_bytes, L.total);
+  QM_CHECK_INIT();
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* b = (uint8_t*)ws;
+  int* ids = (int*)(b + L.ids);
+  float* wts = (float*)(b + L.wts);
+  int* counts = (int*)(b + L.counts);
+  int* cursor = (int*)(b + L.cursor);
+  int* tstart = (int*)(b + L.tstart);
+  int* tiles = (int*)(b + L.tiles);
+  int* stok = (int*)(b + L.stok);
+  float* swt = (float*)(b + L.swt);
+  int* inv = (int*)(b + L.inv);
+  int8_t* hq = (int8_t*)(b + L.hq);
+  float* hsc = (float*)(b + L.hsc);
+  float* y = (float*)(b + L.y);
+  hipError_t e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
+  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
+  if (e == hipSuccess) e = qm::launch_moe_scan(counts, cursor, tstart, tiles, NE, L.tile_rows, s);
+  if (e == hipSuccess) e = qm::launch_moe_scatter(ids, wts, L.slots, NU, cursor, stok, swt, inv, s);
+  if (e == hipSuccess) {
+    qm::GemmArgs a{};
+    a.w = gate->view;
+    a.w2 = up->view;
+    a.aq = aq;
+    a.asc = asc;
+    a.M = L.slots;
+    a.M_stride = M_stride;
+    a.tiles = tiles;
+    a.rowmap = stok;
+    a.hq = hq;
+    a.hsc = hsc;
+    a.slots = L.slots;
+    a.max_tiles = L.max_tiles;
+    a.expert_rows = F;
+    e = qm::launch_gemm(gate->type, qm::GEMM_MOE_GATEUP, a, s);
+  }
+  if (e == hipSuccess) {
+    qm::GemmArgs a{};
+    a.w = down->view;
+    a.aq = hq;
+    a.asc = hsc;
+    a.M = L.slots;
+    a.M_stride = L.slots;
+    a.C = y;
+    a.ldc = E;
+    a.tiles = tiles;
+    a.rowscale = swt;
+    a.slots = L.slots;
+    a.max_tiles = L.max_tiles;
+    a.expert_rows = E;
+    e = qm::launch_gemm(down->type, qm::GEMM_MOE_DOWN, a, s);
+  }
+  if (e == hipSuccess) e = qm::launch_moe_combine(x, y, inv, T, NU, E, accumulate, s);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// Host-side launchers of the qmatmul kernels (one per kernel family, defined next to the kernels).
+// All return hipSuccess or the launch error; shapes are validated by the C-ABI layer (qm_api.hip) beforehand.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qm_device.h"
+
+namespace qm {
+
+// GGUF rows -> prepared planes (qm_prep.hip)
+hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t* qs, uint8_t* hdr, hipStream_t s);
+// f32 rows -> int8 + per-32 scales + per-16 sums (qm_prep.hip)
+hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc,
+                           int16_t* absum, hipStream_t s);
+
+struct GemvArgs {
+  WView w;
+  const int8_t* aq;
+  const float* asc;
+  const int16_t* absum;
+  int M_stride, T;
+  float* C;
+  int ldc, c_off, accumulate;
+  int32_t* dbg_isum;  // non-null: write the block sums instead of C
+  int32_t* dbg_msum;
+};
+hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s);
+
+// Row source of a GEMM's activation tile: dense (row m = token m), gathered (row r = token rowmap[r]) or slots.
+struct GemmArgs {
+  WView w;       // weight (MoE: gate or down, stacked experts)
+  WView w2;      // MoE gate/up: the up projection
+  const int8_t* aq;
+  const float* asc;
+  const int16_t* absum;
+  int M, M_stride;
+  float* C;
+  int ldc, c_off, accumulate;
+  int32_t* dbg_isum;
+  // MoE tile mode
+  const int* tiles;    // [0] = count, then (expert, first slot, rows) per tile
+  const int* rowmap;   // slot -> token (gate/up), or null (down: slot rows)
+  const float* rowscale;  // slot -> routing weight (down), or null
+  int8_t* hq;          // gate/up: quantized h rows [slots][F]
+  float* hsc;          // gate/up: h scales [F/32][slots]
+  int slots;           // row stride of hsc
+  int max_tiles;
+  int expert_rows;     // rows per expert in w (F for gate/up, E for down)
+};
+enum GemmMode : int { GEMM_DENSE = 0, GEMM_MOE_GATEUP = 1, GEMM_MOE_DOWN = 2 };
+hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
+
+// MoE routing (qm_moe.hip)
+hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
+                            hipStream_t s);
+hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s);
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int* cursor, int* stok, float* swt,
+                              int* inv, hipStream_t s);
+hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
+                              hipStream_t s);
+hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s);
+
+}  // namespace qm

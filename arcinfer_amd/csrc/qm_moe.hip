@@ -1,0 +1,179 @@
+// Mixture-of-experts routing and data movement: route (top-k of the router logits), scan (slot ranges and tiles
+// per expert), scatter (device-side token -> slot permutation) and combine (each token's expert outputs summed in
+// selection order). The expert matrices themselves run in qm_gemm.hip's tile modes.
+#include "qm_launch.h"
+
+namespace qm {
+
+// One wave per token: the top NU of the NE logits by repeated arg-max (ties: the lower expert), weights
+// exp(l - max) / sum over the selection (summed in selection order), per-expert counts.
+// zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of 16-lane sub-groups.
+template <int PER_LANE>
+__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int ldl, int T, int NE, int NU,
+                                                    int* __restrict__ ids, float* __restrict__ wts,
+                                                    int* __restrict__ counts) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const float* lg = logits + (size_t)t * ldl;
+  float v[PER_LANE];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    const int e = i * 64 + lane;
+    v[i] = e < NE ? lg[e] : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float sum = 0.0f, my_p = 0.0f;
+  int my_e = 0;
+  for (int k = 0; k < NU; ++k) {
+    float bv = -INFINITY;
+    int bi = NE;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i)
+      if (v[i] > bv) {
+        bv = v[i];
+        bi = i * 64 + lane;
+      }
+    float gv = bv;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
+    int gi = (bv == gv && bi < NE) ? bi : NE;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i)
+      if (i * 64 + lane == gi) v[i] = -INFINITY;
+    const float p = expf(gv - mx);
+    sum += p;
+    if (lane == k) {
+      my_p = p;
+      my_e = gi;
+    }
+  }
+  if (lane < NU) {
+    ids[(size_t)t * NU + lane] = my_e;
+    wts[(size_t)t * NU + lane] = my_p / sum;
+    if (counts) atomicAdd(&counts[my_e], 1);
+  }
+}
+
+hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
+                            hipStream_t s) {
+  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
+  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
+  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
+  return hipGetLastError();
+}
+
+// One work-group of NE threads: exclusive scans of the counts (slot offsets) and of the tile counts
+// (ceil(count / tile_rows)), then the tile list tiles[0] = #tiles, (expert, first slot, rows) per tile.
+// zero/kernels/moe.cl:133-160 (moe_scan).
+__global__ __launch_bounds__(1024) void scan_kernel(const int* __restrict__ counts, int* __restrict__ cursor,
+                                                    int* __restrict__ tstart, int* __restrict__ tiles, int NE,
+                                                    int tile_rows) {
+  __shared__ int sa[1024], sb[1024];
+  const int e = threadIdx.x;
+  const int c = e < NE ? counts[e] : 0, nt = (c + tile_rows - 1) / tile_rows;
+  sa[e] = c;
+  sb[e] = nt;
+  __syncthreads();
+  for (int d = 1; d < (int)blockDim.x; d <<= 1) {
+    const int x = e >= d ? sa[e - d] : 0, y = e >= d ? sb[e - d] : 0;
+    __syncthreads();
+    sa[e] += x;
+    sb[e] += y;
+    __syncthreads();
+  }
+  if (e >= NE) return;
+  const int off = sa[e] - c, toff = sb[e] - nt;
+  cursor[e] = off;
+  tstart[e] = toff;
+  if (e == NE - 1) {
+    tiles[0] = sb[e];
+    tstart[NE] = sb[e];
+  }
+  for (int i = 0; i < nt; ++i) {
+    int* tp = tiles + 1 + 3 * (toff + i);
+    tp[0] = e;
+    tp[1] = off + i * tile_rows;
+    tp[2] = min(tile_rows, c - i * tile_rows);
+  }
+}
+
+hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s) {
+  int threads = 64;
+  while (threads < NE) threads <<= 1;
+  scan_kernel<<<1, threads, 0, s>>>(counts, cursor, tstart, tiles, NE, tile_rows);
+  return hipGetLastError();
+}
+
+// Every (token, k) pair takes the next slot of its expert: slot order within an expert is arbitrary, so every
+// consumer works per slot and the combine reads the slots back through inv in k order.
+// zero/kernels/moe.cl:163-171 (moe_scatter).
+__global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ ids, const float* __restrict__ wts, int n,
+                                                      int NU, int* __restrict__ cursor, int* __restrict__ stok,
+                                                      float* __restrict__ swt, int* __restrict__ inv) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int slot = atomicAdd(&cursor[ids[i]], 1);
+  stok[slot] = i / NU;
+  swt[slot] = wts[i];
+  inv[i] = slot;
+}
+
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int* cursor, int* stok, float* swt,
+                              int* inv, hipStream_t s) {
+  scatter_kernel<<<(n + 255) / 256, 256, 0, s>>>(ids, wts, n, NU, cursor, stok, swt, inv);
+  return hipGetLastError();
+}
+
+// x[t][c] (+)= sum_k y[inv[t*NU + k]][c], k in selection order (zero/kernels/moe.cl:332-340). 4 columns per thread.
+__global__ __launch_bounds__(256) void combine_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                      const int* __restrict__ inv, int T, int NU, int E,
+                                                      int accumulate) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cq = E / 4;
+  if (i >= (long)T * cq) return;
+  const int t = (int)(i / cq), c = (int)(i % cq) * 4;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k = 0; k < NU; ++k) {
+    const float4 u = *(const float4*)(y + (size_t)inv[(size_t)t * NU + k] * E + c);
+    v.x += u.x;
+    v.y += u.y;
+    v.z += u.z;
+    v.w += u.w;
+  }
+  float4* xp = (float4*)(x + (size_t)t * E + c);
+  if (accumulate) {
+    const float4 o = *xp;
+    v.x = o.x + v.x;
+    v.y = o.y + v.y;
+    v.z = o.z + v.z;
+    v.w = o.w + v.w;
+  }
+  *xp = v;
+}
+
+hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
+                              hipStream_t s) {
+  const long n = (long)T * (E / 4);
+  combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, y, inv, T, NU, E, accumulate);
+  return hipGetLastError();
+}
+
+// A fill kernel (not hipMemsetAsync, so the calls stay capturable in HIP graphs).
+__global__ void fill_i32_kernel(int* p, int value, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = value;
+}
+
+hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  fill_i32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, value, n);
+  return hipGetLastError();
+}
+
+}  // namespace qm

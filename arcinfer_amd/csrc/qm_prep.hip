@@ -1,0 +1,121 @@
+// Weight preparation (GGUF -> prepared planes) and the per-32 activation quantizer.
+#include "qm_launch.h"
+
+namespace qm {
+
+// ---------------------------------------------------------------------------------------------------------------
+// One thread per (row, superblock): reads the GGUF superblock bytewise (any alignment) and writes its payload and
+// header into the two planes (layout in qm_device.h). Follows the field offsets of src/quants.h:89-315.
+template <int TYPE>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int rows, int K,
+                                                     uint8_t* __restrict__ qs, uint8_t* __restrict__ hdr) {
+  using Tr = Traits<TYPE>;
+  const int nsb = K / 256;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * nsb) return;
+  const long n = i / nsb;
+  const int s = (int)(i % nsb);
+  const uint8_t* p = raw + ((size_t)n * nsb + s) * Tr::GGUF_SB;
+  uint8_t* q = qs + ((size_t)n * (K / 32) + (size_t)s * 8) * Tr::QB;
+  uint8_t* h = hdr + ((size_t)n * nsb + s) * Tr::HB;
+  if constexpr (TYPE == T_Q8_0) {
+    // 8 GGUF blocks of (f16 d, int8 q[32])
+    for (int b = 0; b < 8; ++b) {
+      h[2 * b] = p[34 * b];
+      h[2 * b + 1] = p[34 * b + 1];
+      for (int e = 0; e < 32; ++e) q[32 * b + e] = p[34 * b + 2 + e];
+    }
+  } else if constexpr (TYPE == T_Q4_K) {
+    // d, dmin, scales[12] | qs[128]: chunk j (64 elements) = qs[32j..32j+31], low nibbles elements 0..31 of the
+    // chunk, high nibbles 32..63. Block 2j takes the low nibbles, 2j+1 the high ones; within a block byte t holds
+    // elements t (low nibble) and 16 + t (high nibble).
+    for (int e = 0; e < 16; ++e) h[e] = p[e];
+    const uint8_t* src = p + 16;
+    for (int j = 0; j < 4; ++j)
+      for (int t = 0; t < 16; ++t) {
+        const uint8_t a = src[32 * j + t], c = src[32 * j + 16 + t];
+        q[16 * (2 * j) + t] = (uint8_t)((a & 0xF) | ((c & 0xF) << 4));
+        q[16 * (2 * j + 1) + t] = (uint8_t)((a >> 4) | ((c >> 4) << 4));
+      }
+  } else if constexpr (TYPE == T_IQ4_XS) {
+    // d, scales_h, scales_l[4] | qs[128] (block ib = qs[16 ib .. 16 ib + 15], already per-32)
+    for (int e = 0; e < 8; ++e) h[e] = p[e];
+    for (int e = 0; e < 128; ++e) q[e] = p[8 + e];
+  } else {  // IQ3_S: d | qs[64] | qh[8] | signs[32] | scales[4]
+    for (int b = 0; b < 8; ++b) {
+      for (int e = 0; e < 8; ++e) q[12 * b + e] = p[2 + 8 * b + e];
+      for (int e = 0; e < 4; ++e) q[12 * b + 8 + e] = p[74 + 4 * b + e];
+    }
+    for (int e = 0; e < 8; ++e) h[e] = p[66 + e];
+    for (int e = 0; e < 4; ++e) h[8 + e] = p[106 + e];
+    h[12] = p[0];
+    h[13] = p[1];
+    h[14] = 0;
+    h[15] = 0;
+  }
+}
+
+hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t* qs, uint8_t* hdr, hipStream_t s) {
+  const long n = (long)rows * (K / 256);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  switch (type) {
+    case T_Q8_0: repack_kernel<T_Q8_0><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_Q4_K: repack_kernel<T_Q4_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Activation quantizer: 8 lanes per 32-block, 4 values per lane. amax is combined over the 8 lanes (max is
+// order-free), then each value is rounded on its own: q = rint(v * (127 / amax)) with IEEE division and
+// round-half-even, the expression of quantize_act_cpu (src/quants.h:559-576) -- bit-exact. Rows m >= M (up to
+// M_stride) are written as zero rows with scale 0.
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int ldx, int M, int M_stride,
+                                                       int K, int8_t* __restrict__ aq, float* __restrict__ asc,
+                                                       int16_t* __restrict__ absum) {
+  const int nb = K / 32;
+  const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;  // one lane = 4 values
+  const long blk = g >> 3;
+  const int sub = (int)(g & 7);
+  const bool live = blk < (long)M_stride * nb;
+  const int m = live ? (int)(blk / nb) : 0;
+  const int b = live ? (int)(blk % nb) : 0;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live && m < M) {
+    const float* src = x + (size_t)m * ldx + 32 * b + 4 * sub;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[i];
+  }
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int sum = 0;
+  uint32_t pk = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = (int)__builtin_rintf(v[i] * inv);
+    sum += q;
+    pk |= (uint32_t)(q & 0xFF) << (8 * i);
+  }
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if (!live) return;
+  *(uint32_t*)(aq + (size_t)m * K + 32 * b + 4 * sub) = pk;
+  if (sub == 0) asc[(size_t)b * M_stride + m] = amax / 127.0f;
+  if ((sub & 3) == 0) absum[(size_t)(2 * b + (sub >> 2)) * M_stride + m] = (int16_t)sum;
+}
+
+hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc,
+                           int16_t* absum, hipStream_t s) {
+  const long lanes = (long)M_stride * (K / 32) * 8;
+  const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
+  quantize_kernel<<<grid, block, 0, s>>>(x, ldx, M, M_stride, K, aq, asc, absum);
+  return hipGetLastError();
+}
+
+}  // namespace qm

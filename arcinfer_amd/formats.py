@@ -1,0 +1,83 @@
+"""GGUF block geometry of the four weight types of the path, and seeded synthetic weights in GGUF block form.
+
+Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_K 256 / 144, IQ3_S 256 / 110,
+IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
+bytes: every quant / index / sign / sub-scale bit uniform, the f16 super-scales |N(0, sigma)|.
+"""
+import numpy as np
+
+Q8_0, Q4_K, IQ3_S, IQ4_XS = 8, 12, 21, 23
+TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
+TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
+
+# bytes of one 256-element superblock (Q8_0: 8 blocks of 34)
+SB_BYTES = {Q8_0: 272, Q4_K: 144, IQ3_S: 110, IQ4_XS: 136}
+
+
+def row_bytes(qtype, K):
+    if K % 256:
+        raise ValueError(f"K = {K} is not a multiple of 256")
+    return K // 256 * SB_BYTES[qtype]
+
+
+def weight_bytes(qtype, N, K):
+    """Algorithmic weight bytes of an N x K matrix: N * (K/256) * superblock bytes."""
+    return N * row_bytes(qtype, K)
+
+
+def f16_bits(x):
+    """float array -> IEEE half bit patterns (round to nearest even), as uint16."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def synth_weight(qtype, N, K, seed, sigma=None):
+    """N rows of K elements in GGUF block form (uint8 [N, row_bytes]).
+
+    Q8_0:   q uniform in [-127, 127], d = f16(|N(0, 0.02)| / 127) per 32 (sigma: the normal's sigma)
+    Q4_K:   quants, 6-bit scales and mins uniform (all bits random), d and dmin = f16(|N(0, 0.01)|)
+    IQ4_XS: nibbles and 6-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
+    IQ3_S:  9-bit grid indices, signs and 4-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
+    """
+    rng = np.random.default_rng(seed)
+    nsb = K // 256
+    if qtype == Q8_0:
+        sig = 0.02 if sigma is None else sigma
+        nblk = N * K // 32
+        blk = np.empty((nblk, 34), dtype=np.uint8)
+        d = f16_bits(np.abs(rng.normal(0.0, sig, nblk)) / 127.0)
+        blk[:, 0] = d & 0xFF
+        blk[:, 1] = d >> 8
+        blk[:, 2:] = rng.integers(-127, 128, size=(nblk, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+        return blk.reshape(N, nsb * 272)
+    sig = 0.01 if sigma is None else sigma
+    sb = SB_BYTES[qtype]
+    raw = rng.integers(0, 256, size=(N * nsb, sb), dtype=np.uint8)
+    d = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
+    raw[:, 0] = d & 0xFF
+    raw[:, 1] = d >> 8
+    if qtype == Q4_K:
+        dm = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
+        raw[:, 2] = dm & 0xFF
+        raw[:, 3] = dm >> 8
+    return raw.reshape(N, nsb * sb)
+
+
+def synth_activations(M, K, seed, outlier_frac=0.0, outlier_scale=20.0):
+    """f32 [M, K] N(0, 1); with outlier_frac > 0 a fixed seeded set of that fraction of the channels x outlier_scale."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    if outlier_frac > 0:
+        n_out = max(1, int(round(K * outlier_frac)))
+        ch = rng.choice(K, size=n_out, replace=False)
+        x[:, ch] *= np.float32(outlier_scale)
+    return x
+
+
+def zipf_router_logits(T, NE, seed, s=1.1):
+    """Router logits whose top-8 is Zipf(s)-distributed over the experts: logit_e = -s * ln(rank_e) + Gumbel(0, 1),
+    with a seeded random rank permutation (top-k of Gumbel-perturbed log-weights samples k distinct experts with
+    probability proportional to rank^-s)."""
+    rng = np.random.default_rng(seed)
+    rank = rng.permutation(NE) + 1
+    g = rng.gumbel(0.0, 1.0, size=(T, NE))
+    return (-s * np.log(rank)[None, :] + g).astype(np.float32)

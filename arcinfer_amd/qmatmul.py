@@ -1,0 +1,215 @@
+"""ctypes binding of libqmatmul.so (include/qmatmul.h) and torch-tensor conveniences.
+
+The library is the product: this module only passes device pointers and sizes through the C ABI. It raises
+QMatmulError for any non-zero status, and refuses to run when the library is not built (there is no fallback).
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqmatmul.so")
+
+QM_OK = 0
+STATUS_NAMES = {0: "QM_OK", 1: "QM_ERR_ARG", 2: "QM_ERR_SHAPE", 3: "QM_ERR_TYPE", 4: "QM_ERR_HIP",
+                5: "QM_ERR_NOMEM", 6: "QM_ERR_WORKSPACE"}
+
+# every function include/qmatmul.h declares: (name, restype, argtypes)
+_c = ctypes
+_P = _c.c_void_p
+_I = _c.c_int
+_Z = _c.c_size_t
+SIGNATURES = [
+    ("qmatmul_init", _I, []),
+    ("qmatmul_last_error", _c.c_char_p, []),
+    ("qmatmul_sb_bytes", _Z, [_I]),
+    ("qmatmul_weight_bytes", _Z, [_I, _I, _I]),
+    ("qmatmul_prepare_weight", _I, [_I, _P, _I, _I, _I, _P, _c.POINTER(_P)]),
+    ("qmatmul_release_weight", _I, [_P]),
+    ("qmatmul_weight_info", _I, [_P, _c.POINTER(_I), _c.POINTER(_I), _c.POINTER(_I)]),
+    ("qmatmul_quantize_act", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_gemv", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    ("qmatmul_gemm", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    ("qmatmul_moe_workspace_size", _Z, [_I, _I, _I, _I, _I]),
+    ("qmatmul_moe_route", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_moe_grouped", _I, [_P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _Z, _P]),
+    ("qmatmul_moe_ws_layout", _I, [_I, _I, _I, _I, _I, _P]),
+    ("qmatmul_gemv_blocksums", _I, [_P, _P, _P, _I, _I, _P, _P, _P]),
+    ("qmatmul_gemm_blocksums", _I, [_P, _P, _I, _I, _P, _P]),
+]
+
+
+class QMatmulError(RuntimeError):
+    def __init__(self, fn, status, msg):
+        super().__init__(f"{fn}: {STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+class MoeWsLayout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ("ids", "wts", "counts", "cursor", "tstart", "tiles", "stok", "swt", "inv", "hq", "hsc", "y",
+                 "total")] + [("slots", ctypes.c_int), ("max_tiles", ctypes.c_int), ("tile_rows", ctypes.c_int)]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Loads libqmatmul.so (built in-tree by arcinfer_amd.build); raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `python -m arcinfer_amd.build` (there is no fallback path)")
+    # One HIP runtime per process: torch ships its own libamdhip64.so.7 and loads it under another file name, so
+    # it must be loaded first; the library's libamdhip64.so.7 dependency then binds to that copy (by soname)
+    # instead of bringing in /opt/rocm's as a second runtime that would not know torch's memory and streams.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(path)
+    for name, res, args in SIGNATURES:
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _call(name, *args):
+    lib = load_library()
+    st = getattr(lib, name)(*args)
+    if st != QM_OK:
+        raise QMatmulError(name, st, lib.qmatmul_last_error().decode())
+    return st
+
+
+# ---- torch helpers ------------------------------------------------------------------------------------------------
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class QWeight:
+    """A prepared weight (qm_weight*) from GGUF bytes: a uint8 tensor (device or CPU) or a numpy array."""
+
+    def __init__(self, qtype, raw, rows, K, stream=None):
+        import numpy as np
+        import torch
+        self.qtype, self.rows, self.K = int(qtype), int(rows), int(K)
+        h = ctypes.c_void_p()
+        if isinstance(raw, np.ndarray):
+            raw = np.ascontiguousarray(raw)
+            _call("qmatmul_prepare_weight", self.qtype, ctypes.c_void_p(raw.ctypes.data), 0, self.rows, self.K,
+                  _stream(stream), ctypes.byref(h))
+        else:
+            assert isinstance(raw, torch.Tensor) and raw.is_contiguous()
+            _call("qmatmul_prepare_weight", self.qtype, _ptr(raw), 1 if raw.is_cuda else 0, self.rows, self.K,
+                  _stream(stream), ctypes.byref(h))
+        self.handle = h
+
+    @property
+    def nbytes(self):
+        return load_library().qmatmul_weight_bytes(self.qtype, self.rows, self.K)
+
+    def release(self):
+        if self.handle:
+            _call("qmatmul_release_weight", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.qmatmul_release_weight(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def quantize_act(x, M_stride=None, stream=None):
+    """x f32 [M, K] (cuda) -> (aq int8 [M_stride, K], asc f32 [K/32, M_stride], absum int16 [K/16, M_stride])."""
+    import torch
+    M, K = x.shape
+    Ms = M if M_stride is None else M_stride
+    aq = torch.empty((Ms, K), dtype=torch.int8, device=x.device)
+    asc = torch.empty((K // 32, Ms), dtype=torch.float32, device=x.device)
+    absum = torch.empty((K // 16, Ms), dtype=torch.int16, device=x.device)
+    _call("qmatmul_quantize_act", _ptr(x), x.stride(0), M, Ms, K, _ptr(aq), _ptr(asc), _ptr(absum), _stream(stream))
+    return aq, asc, absum
+
+
+def gemv(w, aq, asc, absum, T=1, C=None, ldc=None, c_off=0, accumulate=0, stream=None):
+    import torch
+    Ms = aq.shape[0]
+    if C is None:
+        C = torch.empty((T, w.rows), dtype=torch.float32, device=aq.device)
+        ldc = w.rows
+    _call("qmatmul_gemv", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), Ms, T, _ptr(C),
+          w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
+    return C
+
+
+def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None):
+    import torch
+    Ms = aq.shape[0]
+    M = Ms if M is None else M
+    if C is None:
+        C = torch.empty((M, w.rows), dtype=torch.float32, device=aq.device)
+        ldc = w.rows
+    _call("qmatmul_gemm", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, _ptr(C),
+          w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
+    return C
+
+
+def gemv_blocksums(w, aq, absum, T=1, stream=None):
+    import torch
+    nb = w.K // 32
+    isum = torch.empty((T, w.rows, nb), dtype=torch.int32, device=aq.device)
+    msum = torch.empty((T, w.rows, nb), dtype=torch.int32, device=aq.device) if w.qtype == 12 else None
+    _call("qmatmul_gemv_blocksums", w.handle, _ptr(aq), _ptr(absum), aq.shape[0], T, _ptr(isum), _ptr(msum),
+          _stream(stream))
+    return isum, msum
+
+
+def gemm_blocksums(w, aq, M=None, stream=None):
+    import torch
+    M = aq.shape[0] if M is None else M
+    isum = torch.empty((M, w.rows, w.K // 32), dtype=torch.int32, device=aq.device)
+    _call("qmatmul_gemm_blocksums", w.handle, _ptr(aq), M, aq.shape[0], _ptr(isum), _stream(stream))
+    return isum
+
+
+def moe_route(logits, NU, NE=None, stream=None):
+    import torch
+    T, ldl = logits.shape
+    NE = ldl if NE is None else NE
+    ids = torch.empty((T, NU), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((T, NU), dtype=torch.float32, device=logits.device)
+    counts = torch.empty((NE,), dtype=torch.int32, device=logits.device)
+    _call("qmatmul_moe_route", _ptr(logits), ldl, T, NE, NU, _ptr(ids), _ptr(wts), _ptr(counts), _stream(stream))
+    return ids, wts, counts
+
+
+def moe_ws_layout(T, NE, NU, E, F):
+    L = MoeWsLayout()
+    _call("qmatmul_moe_ws_layout", T, NE, NU, E, F, ctypes.byref(L))
+    return L
+
+
+def moe_workspace(T, NE, NU, E, F, device="cuda"):
+    import torch
+    n = load_library().qmatmul_moe_workspace_size(T, NE, NU, E, F)
+    return torch.empty((n,), dtype=torch.uint8, device=device)
+
+
+def moe_grouped(gate, up, down, NE, logits, NU, aq, asc, x, ws, T=None, accumulate=0, stream=None):
+    T = logits.shape[0] if T is None else T
+    _call("qmatmul_moe_grouped", gate.handle, up.handle, down.handle, NE, _ptr(logits), logits.stride(0), T, NU,
+          _ptr(aq), _ptr(asc), aq.shape[0], _ptr(x), accumulate, _ptr(ws), ws.numel(), _stream(stream))
+    return x

@@ -1,0 +1,136 @@
+/* qmatmul -- MI355X (gfx950) quantized matrix products for GGUF weights: the C ABI.
+ *
+ * The drop-in boundary for arcinferzero's quantized matmul path (rizagp/arcinfer). Plain C: device pointers,
+ * sizes and status codes; no C++ or HIP types. `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ * Every call is stream-ordered and asynchronous (no host synchronisation inside), except qmatmul_prepare_weight with
+ * a host source, which copies synchronously. Calls never throw or exit: they return a qm_status and leave a message
+ * for qmatmul_last_error() (thread-local).
+ *
+ * Activation layout (the reference's quant_store16 layout, zero/kernels/ops.cl:18-77, act32):
+ *   aq    int8  [M_stride][K]   row-major, one row per token
+ *   asc   float [K/32][M_stride] scale of each 32-block, token fastest
+ *   absum int16 [K/16][M_stride] sum of each 16-block's int8 values, token fastest (needed by Q4_K only)
+ * Rows M..M_stride-1 of a padded batch are zero rows.
+ *
+ * Weights: GGUF blocks, rows of K elements, K a multiple of 256 (Q8_0: 8 blocks of 32 per 256). A weight is
+ * prepared once (qmatmul_prepare_weight) into this library's own device layout and then read by every product.
+ *
+ * accumulate (all products): 0 = store, 1 = C += result, 2 = C = silu(C) * result (GEMM only, fused SwiGLU:
+ * C holds the gate projection), as zero/kernels/gemm.cl:464-471.
+ */
+#ifndef QMATMUL_H
+#define QMATMUL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
+typedef enum { QM_Q8_0 = 8, QM_Q4_K = 12, QM_IQ3_S = 21, QM_IQ4_XS = 23 } qm_type;
+
+typedef enum {
+  QM_OK = 0,
+  QM_ERR_ARG = 1,       /* null pointer or invalid argument */
+  QM_ERR_SHAPE = 2,     /* a shape the kernels do not cover (the reference throws runtime_error here,
+                           zero/engine.h:3255-3257) */
+  QM_ERR_TYPE = 3,      /* weight type not supported by this entry point */
+  QM_ERR_HIP = 4,       /* a HIP runtime call failed (message holds hipGetErrorString) */
+  QM_ERR_NOMEM = 5,     /* device allocation failed */
+  QM_ERR_WORKSPACE = 6  /* workspace too small */
+} qm_status;
+
+typedef struct qm_weight qm_weight; /* opaque: a prepared (device-resident) weight matrix */
+
+/* Per-device one-time set-up (codebooks to the device). Optional: every entry point calls it on first use.
+ * Replaces the table upload of Engine::build_kernels (zero/engine.h:1921-1922, src/quants.h:622-634). */
+int qmatmul_init(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qmatmul_last_error(void);
+
+/* Bytes of one 256-element superblock in GGUF (0 for an unsupported type); src/gguf.h:43-72. */
+size_t qmatmul_sb_bytes(int type);
+
+/* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S superblock). */
+size_t qmatmul_weight_bytes(int type, int rows, int K);
+
+/* Prepares a weight from its GGUF bytes: rows x (K/256) superblocks, row-major, as stored in a GGUF tensor (a
+ * stacked expert tensor [NE][N][K] is NE*N rows). raw is a device pointer if raw_on_device, else a host pointer.
+ * Allocates the prepared copy and returns it in *out. Replaces Engine::make_weight / upload_padded
+ * (zero/engine.h:1936-2014; src/quants.h:643-681). */
+int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int rows, int K, void* stream,
+                           qm_weight** out);
+
+/* Frees a prepared weight (waits for the device). */
+int qmatmul_release_weight(qm_weight* w);
+
+/* Type, rows and K of a prepared weight (any output pointer may be NULL). */
+int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K);
+
+/* Activation quantizer: x f32 [M][ldx] -> aq, asc, absum (layout above; rows M..M_stride-1 zeroed).
+ * Per 32 values: amax = max |v|; asc = amax / 127; q = round-half-even(v * (127 / amax)), 0 if amax == 0;
+ * absum = sum of q per 16. Bit-exact with quantize_act_cpu(act32 = true), src/quants.h:559-576, which is the CPU
+ * twin of quant_store16 (zero/kernels/ops.cl:18-77) as rmsnorm_quant / swiglu_quant(fused=1) use it
+ * (zero/engine.h:3302-3308, 3451-3456). K % 32 == 0. */
+int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
+                         void* stream);
+
+/* Decode GEMV, T tokens (1..8) against one read of the weight:
+ *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
+ * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K only.
+ * Replaces the gemv / gemv_v / gemv_mt / gemv_mt_v launches of Engine::matmul1 (zero/engine.h:3184-3232;
+ * zero/kernels/decode.cl:636-737, 1074-1141, 1145-1411). */
+int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,
+                 float* C, int ldc, int c_off, int accumulate, void* stream);
+
+/* Prompt GEMM on int8 MFMA: C[m*ldc + c_off + n] (op)= sum_k W[n][k] * a_m[k] for m < M.
+ * M <= M_stride; any M >= 1 and rows(w) % 16 == 0. Replaces decode_w8 + gemm of Engine::matmul1 for T > 8 and
+ * gemm_ext (zero/engine.h:3234-3297; zero/kernels/gemm.cl:132-475). Q4_K is computed exactly (scales and mins),
+ * not requantized as the reference's W8 path does (zero/kernels/decode.cl:455-507). */
+int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                 float* C, int ldc, int c_off, int accumulate, void* stream);
+
+/* Workspace bytes of qmatmul_moe_grouped for T tokens, NE experts, NU experts per token, hidden E, expert width F. */
+size_t qmatmul_moe_workspace_size(int T, int NE, int NU, int E, int F);
+
+/* Routing alone (test and reuse): top NU of each token's NE logits (row stride ldl; ties go to the lower expert),
+ * weights exp(l - max) / sum over the selection, per-expert counts (counts is overwritten).
+ * zero/kernels/moe.cl:42-81 (moe_route). */
+int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
+                      void* stream);
+
+/* Mixture-of-experts FFN over T tokens (Qwen3.5-MoE style), the expert part of Engine::layer_moe
+ * (zero/engine_moe.h:8-282):
+ *   x[t][:E] (op)= sum_k w_tk * down_e( q( silu(gate_e(a_t)) * up_e(a_t) ) ),  e = k-th expert of token t
+ * gate, up: NE*F rows of E; down: NE*E rows of F (stacked experts). a_t: token t of aq/asc (E values). q(): the h
+ * rows quantized per 32 as moe_quant (moe.cl:251-282). Route, exclusive scan into tiles, device-side scatter of
+ * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
+ * order (moe.cl:332-340). Gate/up/down types without per-block mins (Q8_0, IQ4_XS, IQ3_S). accumulate 0 or 1.
+ * ws: device workspace of at least qmatmul_moe_workspace_size bytes (layout: qmatmul_moe_ws_layout). */
+int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
+                        int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,
+                        int accumulate, void* ws, size_t ws_bytes, void* stream);
+
+/* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). */
+typedef struct {
+  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, total;
+  int slots, max_tiles, tile_rows;
+} qm_moe_ws_layout;
+int qmatmul_moe_ws_layout(int T, int NE, int NU, int E, int F, qm_moe_ws_layout* out);
+
+/* Verification hooks: the integer block sums of the GEMV / GEMM kernels, from the same decode and dot-product
+ * code as the products. For each token m < M, row n and 32-block b (index (m*rows + n)*(K/32) + b):
+ *   isum[...] = sc_b * sum_{k in b} q[n][k] * a_m[k]   (Q8_0: sc_b = 1)
+ *   msum[...] = mn_b * (absum of the block's two 16-halves)   (Q4_K only; NULL otherwise)
+ * These are the reference's `sc0 * lo + sc1 * hi` and `mn0 * bs0 + mn1 * bs1` (zero/kernels/decode.cl:695-706). */
+int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* absum, int M_stride, int T,
+                           int32_t* isum, int32_t* msum, void* stream);
+int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMATMUL_H */

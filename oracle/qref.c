@@ -1,0 +1,416 @@
+/* CPU oracle for the quantized matrix-product path -- TEST INFRASTRUCTURE ONLY (see qref.h).
+ *
+ * Compiled with -ffp-contract=off and without fast-math, so float expressions round exactly as written.
+ * Reference citations are rizagp/arcinfer paths relative to its root.
+ */
+#include "qref.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static const uint32_t k_iq3s_grid[512] = QM_IQ3S_GRID_INIT;
+static const int8_t k_iq4nl[16] = QM_IQ4NL_VALUES_INIT;
+
+/* src/quants.h:17-31 -- IEEE half to float, subnormals normalised by shifting */
+float qref_fp16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, f;
+  if (e == 0) {
+    if (m == 0) {
+      f = sign;
+    } else {
+      e = 127 - 15 + 1;
+      while (!(m & 0x400u)) {
+        m <<= 1;
+        --e;
+      }
+      f = sign | (e << 23) | ((m & 0x3FFu) << 13);
+    }
+  } else if (e == 31) {
+    f = sign | 0x7F800000u | (m << 13);
+  } else {
+    f = sign | ((e + 127 - 15) << 23) | (m << 13);
+  }
+  float r;
+  memcpy(&r, &f, 4);
+  return r;
+}
+
+/* src/quants.h:33-52 -- float to half, round to nearest even, NaN kept quiet, overflow to infinity */
+uint16_t qref_f32_to_fp16(float x) {
+  uint32_t f;
+  memcpy(&f, &x, 4);
+  const uint32_t sign = (f >> 16) & 0x8000u;
+  const int32_t e = (int32_t)((f >> 23) & 0xFFu) - 127 + 15;
+  uint32_t m = f & 0x7FFFFFu;
+  if (((f >> 23) & 0xFFu) == 0xFFu) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
+  if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    m |= 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)h;
+}
+
+/* src/gguf.h:43-72 (the four types of this path) */
+int qref_block_info(int type, int* blk, int* bytes) {
+  switch (type) {
+    case QREF_Q8_0: *blk = 32; *bytes = 34; return 0;
+    case QREF_Q4_K: *blk = 256; *bytes = 144; return 0;
+    case QREF_IQ3_S: *blk = 256; *bytes = 110; return 0;
+    case QREF_IQ4_XS: *blk = 256; *bytes = 136; return 0;
+    default: return -1;
+  }
+}
+
+int qref_sb_bytes(int type) {
+  int blk, bytes;
+  if (qref_block_info(type, &blk, &bytes)) return -1;
+  return bytes * (256 / blk);
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* src/quants.h:61-69 */
+static void scale_min_k4(int j, const uint8_t* q, int* d, int* m) {
+  if (j < 4) {
+    *d = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    *m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
+  }
+}
+
+/* src/quants.h:89-315 (cases Q4_K 91-114, Q8_0 149-158, IQ3_S 240-262, IQ4_XS 297-312) */
+int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
+  memset(o, 0, sizeof(*o));
+  switch (type) {
+    case QREF_Q4_K: {
+      o->d = qref_fp16_to_f32(rd16(p));
+      o->dmin = qref_fp16_to_f32(rd16(p + 2));
+      for (int b = 0; b < 8; ++b) scale_min_k4(b, p + 4, &o->sc[b], &o->mn[b]);
+      const uint8_t* qs = p + 16;
+      for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+          o->q[64 * j + l] = (int16_t)(qs[32 * j + l] & 0xF);
+          o->q[64 * j + 32 + l] = (int16_t)(qs[32 * j + l] >> 4);
+        }
+      return 0;
+    }
+    case QREF_Q8_0: {
+      for (int b = 0; b < 8; ++b) {
+        const uint8_t* blk = p + 34 * b;
+        o->d8[b] = qref_fp16_to_f32(rd16(blk));
+        o->sc[b] = 1;
+        for (int i = 0; i < 32; ++i) o->q[32 * b + i] = (int16_t)(int8_t)blk[2 + i];
+      }
+      return 0;
+    }
+    case QREF_IQ3_S: {
+      o->d = qref_fp16_to_f32(rd16(p));
+      const uint8_t *qs = p + 2, *qh = p + 66, *signs = p + 74, *scales = p + 106;
+      for (int ib = 0; ib < 8; ++ib) {
+        o->sc[ib] = 1 + 2 * ((scales[ib / 2] >> (4 * (ib % 2))) & 0xF);
+        const unsigned h = qh[ib];
+        for (int l = 0; l < 4; ++l) {
+          const uint32_t g1 = k_iq3s_grid[qs[8 * ib + 2 * l] | ((h << (8 - 2 * l)) & 256)];
+          const uint32_t g2 = k_iq3s_grid[qs[8 * ib + 2 * l + 1] | ((h << (7 - 2 * l)) & 256)];
+          const unsigned sg = signs[4 * ib + l];
+          for (int j = 0; j < 4; ++j) {
+            const int v1 = (int)((g1 >> (8 * j)) & 0xFF), v2 = (int)((g2 >> (8 * j)) & 0xFF);
+            o->q[32 * ib + 8 * l + j] = (int16_t)((sg & (1u << j)) ? -v1 : v1);
+            o->q[32 * ib + 8 * l + j + 4] = (int16_t)((sg & (1u << (j + 4))) ? -v2 : v2);
+          }
+        }
+      }
+      return 0;
+    }
+    case QREF_IQ4_XS: {
+      o->d = qref_fp16_to_f32(rd16(p));
+      const unsigned sh = rd16(p + 2);
+      const uint8_t *sl = p + 4, *qs = p + 8;
+      for (int ib = 0; ib < 8; ++ib) {
+        const int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0xF) | (int)(((sh >> (2 * ib)) & 3) << 4);
+        o->sc[ib] = ls - 32;
+        for (int j = 0; j < 16; ++j) {
+          o->q[32 * ib + j] = k_iq4nl[qs[16 * ib + j] & 0xF];
+          o->q[32 * ib + 16 + j] = k_iq4nl[qs[16 * ib + j] >> 4];
+        }
+      }
+      return 0;
+    }
+    default: return -1;
+  }
+}
+
+/* src/quants.h:317-324 (dequant_value) via :496-555 (dequant_row): float expressions as written there */
+static float dequant_value(int type, const qref_sb* o, int e) {
+  switch (type) {
+    case QREF_Q4_K: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - o->dmin * (float)o->mn[e / 32];
+    case QREF_Q8_0: return o->d8[e / 32] * (float)o->q[e];
+    default: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - 0.0f;
+  }
+}
+
+int qref_dequant_row(int type, const uint8_t* row, int K, float* out) {
+  const int sb = qref_sb_bytes(type);
+  if (sb < 0 || K % 256) return -1;
+  qref_sb o;
+  for (int s = 0; s < K / 256; ++s) {
+    qref_decode_sb(type, row + (size_t)s * sb, &o);
+    for (int e = 0; e < 256; ++e) out[s * 256 + e] = dequant_value(type, &o, e);
+  }
+  return 0;
+}
+
+/* src/quants.h:559-576 (quantize_act_cpu); zero rows past M as rmsnorm_quant writes them (ops.cl:82-104) */
+void qref_quantize_act(const float* x, int M, int K, int M_stride, int act32, int8_t* aq, float* asc, int16_t* absum) {
+  const int B = act32 ? 32 : 256;
+  for (int m = 0; m < M_stride; ++m)
+    for (int b0 = 0; b0 < K; b0 += B) {
+      float amax = 0.0f;
+      if (m < M)
+        for (int i = 0; i < B; ++i) amax = fmaxf(amax, fabsf(x[(size_t)m * K + b0 + i]));
+      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+      asc[(size_t)(b0 / B) * M_stride + m] = amax / 127.0f;
+      for (int i = 0; i < B; ++i)
+        aq[(size_t)m * K + b0 + i] = m < M ? (int8_t)lrintf(x[(size_t)m * K + b0 + i] * inv) : 0;
+    }
+  for (int m = 0; m < M_stride; ++m)
+    for (int b = 0; b < K / 16; ++b) {
+      int sum = 0;
+      for (int i = 0; i < 16; ++i) sum += aq[(size_t)m * K + b * 16 + i];
+      absum[(size_t)b * M_stride + m] = (int16_t)sum;
+    }
+}
+
+/* One row's superblocks decoded once: int8 quants and per-32 integer scales / float superblock scales. */
+typedef struct {
+  int8_t* q;   /* [K] */
+  int* sc;     /* [K/32] */
+  int* mn;     /* [K/32] */
+  float* d;    /* [K/32]: d of the block's superblock (Q8_0: the block's own scale) */
+  float* dmin; /* [K/32] */
+} row_dec;
+
+static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
+  const int sb = qref_sb_bytes(type);
+  qref_sb o;
+  for (int s = 0; s < K / 256; ++s) {
+    qref_decode_sb(type, row + (size_t)s * sb, &o);
+    for (int e = 0; e < 256; ++e) r->q[s * 256 + e] = (int8_t)o.q[e];
+    for (int b = 0; b < 8; ++b) {
+      r->sc[s * 8 + b] = o.sc[b];
+      r->mn[s * 8 + b] = o.mn[b];
+      r->d[s * 8 + b] = type == QREF_Q8_0 ? o.d8[b] : o.d;
+      r->dmin[s * 8 + b] = o.dmin;
+    }
+  }
+}
+
+/* decode.cl:695-706 (gemv) and 1107-1115 (gemv_v): per 32-block, int sums of int8 products; the block's value
+ * sa * d * (float)(sc0 * lo + sc1 * hi) [- sa * dmin * (float)(mn0 * bs0 + mn1 * bs1) for Q4_K]; here sc0 = sc1
+ * and mn0 = mn1 for all four types (scales per 32), so sc0 * lo + sc1 * hi = sc * (lo + hi). */
+static double row_dot(int type, const row_dec* r, int K, const int8_t* a, const float* asc, const int16_t* absum,
+                      int m, int M_stride, int32_t* bsums, int32_t* msums) {
+  double acc = 0.0;
+  for (int b = 0; b < K / 32; ++b) {
+    int isum = 0;
+    for (int i = 0; i < 32; ++i) isum += (int)a[32 * b + i] * (int)r->q[32 * b + i];
+    const int iv = r->sc[b] * isum;
+    const float sa = asc[(size_t)b * M_stride + m];
+    float v;
+    if (type == QREF_Q4_K) {
+      const int bs = (int)absum[(size_t)(2 * b) * M_stride + m] + (int)absum[(size_t)(2 * b + 1) * M_stride + m];
+      const int mv = r->mn[b] * bs;
+      v = sa * (r->d[b] * (float)iv - r->dmin[b] * (float)mv);
+      if (msums) msums[b] = mv;
+    } else {
+      v = sa * r->d[b] * (float)iv;
+    }
+    if (bsums) bsums[b] = iv;
+    acc += (double)v;
+  }
+  return acc;
+}
+
+int qref_blockdot(int type, const uint8_t* W, int N, int K, const int8_t* aq, const float* asc, const int16_t* absum,
+                  int M, int M_stride, float* C, int ldc, int32_t* blocksums, int32_t* minsums, int n_col_stride,
+                  int nthreads) {
+  const int sb = qref_sb_bytes(type);
+  if (sb < 0 || K % 256 || M > M_stride || n_col_stride < 1) return -1;
+  const size_t rb = (size_t)(K / 256) * sb;
+  const int nb = K / 32;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+#endif
+  {
+    row_dec r;
+    r.q = (int8_t*)malloc((size_t)K);
+    r.sc = (int*)malloc(sizeof(int) * nb);
+    r.mn = (int*)malloc(sizeof(int) * nb);
+    r.d = (float*)malloc(sizeof(float) * nb);
+    r.dmin = (float*)malloc(sizeof(float) * nb);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+    for (int n = 0; n < N; n += n_col_stride) {
+      decode_row(type, W + (size_t)n * rb, K, &r);
+      for (int m = 0; m < M; ++m) {
+        int32_t* bs = blocksums ? blocksums + ((size_t)m * N + n) * nb : NULL;
+        int32_t* ms = minsums ? minsums + ((size_t)m * N + n) * nb : NULL;
+        C[(size_t)m * ldc + n] = (float)row_dot(type, &r, K, aq + (size_t)m * K, asc, absum, m, M_stride, bs, ms);
+      }
+    }
+    free(r.q);
+    free(r.sc);
+    free(r.mn);
+    free(r.d);
+    free(r.dmin);
+  }
+  return 0;
+}
+
+/* tools/ref_forward.cpp:137-159 -- dequant_row, then double dot products */
+int qref_matmul_f32(int type, const uint8_t* W, int N, int K, const float* X, int M, float* Y, int nthreads) {
+  const int sb = qref_sb_bytes(type);
+  if (sb < 0 || K % 256) return -1;
+  const size_t rb = (size_t)(K / 256) * sb;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+#endif
+  {
+    float* w = (float*)malloc(sizeof(float) * (size_t)K);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 16)
+#endif
+    for (int n = 0; n < N; ++n) {
+      qref_dequant_row(type, W + (size_t)n * rb, K, w);
+      for (int m = 0; m < M; ++m) {
+        double acc = 0.0;
+        const float* x = X + (size_t)m * K;
+        for (int k = 0; k < K; ++k) acc += (double)w[k] * (double)x[k];
+        Y[(size_t)m * N + n] = (float)acc;
+      }
+    }
+    free(w);
+  }
+  return 0;
+}
+
+/* zero/kernels/moe.cl:42-81 (moe_route): repeated arg-max over the logits (ties: the lower expert), p = exp(l - max)
+ * in float, weights p / sum over the selection (sum in selection order) */
+void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts) {
+  if (counts)
+    for (int e = 0; e < NE; ++e) counts[e] = 0;
+  char* taken = (char*)malloc((size_t)NE);
+  for (int t = 0; t < T; ++t) {
+    const float* l = logits + (size_t)t * ldl;
+    float mx = -INFINITY;
+    for (int e = 0; e < NE; ++e) mx = fmaxf(mx, l[e]);
+    memset(taken, 0, (size_t)NE);
+    float p[64], sum = 0.0f;
+    for (int k = 0; k < NU; ++k) {
+      int bi = -1;
+      for (int e = 0; e < NE; ++e)
+        if (!taken[e] && (bi < 0 || l[e] > l[bi])) bi = e;
+      taken[bi] = 1;
+      ids[(size_t)t * NU + k] = bi;
+      p[k] = expf(l[bi] - mx);
+      sum += p[k];
+      if (counts) ++counts[bi];
+    }
+    for (int k = 0; k < NU; ++k) wts[(size_t)t * NU + k] = p[k] / sum;
+  }
+  free(taken);
+}
+
+int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
+                     const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
+                     const int8_t* aq, const float* asc, int M_stride, float* x, int accumulate, int nthreads) {
+  const int sbg = qref_sb_bytes(type_gate), sbu = qref_sb_bytes(type_up), sbd = qref_sb_bytes(type_down);
+  if (sbg < 0 || sbu < 0 || sbd < 0 || E % 256 || F % 256 || NU > 64 || T > M_stride) return -1;
+  /* (types with per-block mins need the activation sums, which the expert path does not carry: the reference's
+   *  expert GEMM takes no min types either, zero/engine_moe.h:284-289) */
+  if (type_gate == QREF_Q4_K || type_up == QREF_Q4_K || type_down == QREF_Q4_K) return -1;
+  int* ids = (int*)malloc(sizeof(int) * (size_t)T * NU);
+  float* wts = (float*)malloc(sizeof(float) * (size_t)T * NU);
+  qref_moe_route(logits, ldl, T, NE, NU, ids, wts, NULL);
+  const size_t rbg = (size_t)(E / 256) * sbg, rbu = (size_t)(E / 256) * sbu, rbd = (size_t)(F / 256) * sbd;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+#endif
+  {
+    row_dec r;
+    const int KM = E > F ? E : F;
+    r.q = (int8_t*)malloc((size_t)KM);
+    r.sc = (int*)malloc(sizeof(int) * KM / 32);
+    r.mn = (int*)malloc(sizeof(int) * KM / 32);
+    r.d = (float*)malloc(sizeof(float) * KM / 32);
+    r.dmin = (float*)malloc(sizeof(float) * KM / 32);
+    float* h = (float*)malloc(sizeof(float) * F);
+    int8_t* hq = (int8_t*)malloc((size_t)F);
+    float* hsc = (float*)malloc(sizeof(float) * F / 32);
+    int16_t* hab = (int16_t*)malloc(sizeof(int16_t) * F / 16);
+    float* y = (float*)malloc(sizeof(float) * (size_t)NU * E);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+    for (int t = 0; t < T; ++t) {
+      for (int k = 0; k < NU; ++k) {
+        const int e = ids[(size_t)t * NU + k];
+        /* gate / up: h = up * silu(gate) as gemm.cl:464-471 (accumulate 2) */
+        for (int f = 0; f < F; ++f) {
+          decode_row(type_gate, Wg + ((size_t)e * F + f) * rbg, E, &r);
+          const float g = (float)row_dot(type_gate, &r, E, aq + (size_t)t * E, asc, NULL, t, M_stride, NULL, NULL);
+          decode_row(type_up, Wu + ((size_t)e * F + f) * rbu, E, &r);
+          const float u = (float)row_dot(type_up, &r, E, aq + (size_t)t * E, asc, NULL, t, M_stride, NULL, NULL);
+          h[f] = u * (g / (1.0f + expf(-g)));
+        }
+        /* moe.cl:251-282: h quantized per 32 */
+        qref_quantize_act(h, 1, F, 1, 1, hq, hsc, hab);
+        /* down, times the routing weight (moe.cl:327) */
+        const float w = wts[(size_t)t * NU + k];
+        for (int c = 0; c < E; ++c) {
+          decode_row(type_down, Wd + ((size_t)e * E + c) * rbd, F, &r);
+          const float v = (float)row_dot(type_down, &r, F, hq, hsc, hab, 0, 1, NULL, NULL);
+          y[(size_t)k * E + c] = w * v;
+        }
+      }
+      /* moe.cl:332-340: the token's NU outputs summed in selection order */
+      for (int c = 0; c < E; ++c) {
+        float v = 0.0f;
+        for (int k = 0; k < NU; ++k) v += y[(size_t)k * E + c];
+        x[(size_t)t * E + c] = accumulate ? x[(size_t)t * E + c] + v : v;
+      }
+    }
+    free(r.q);
+    free(r.sc);
+    free(r.mn);
+    free(r.d);
+    free(r.dmin);
+    free(h);
+    free(hq);
+    free(hsc);
+    free(hab);
+    free(y);
+  }
+  free(ids);
+  free(wts);
+  return 0;
+}

@@ -1,0 +1,65 @@
+"""Independent numpy encoders of the four GGUF block structs, written from the GGML block definitions
+(ggml-common.h: block_q8_0 {d; qs[32]}, block_q4_K {d; dmin; scales[12]; qs[128]}, block_iq4_xs {d; scales_h;
+scales_l[4]; qs[128]}, block_iq3_s {d; qs[64]; qh[8]; signs[32]; scales[4]}), NOT from the oracle's decoders: they
+pack chosen integer fields into bytes, so decoding them back pins the decoders' bit positions."""
+import numpy as np
+
+
+def _h(d):
+    return np.array([d], dtype=np.float16).view(np.uint8)
+
+
+def enc_q8_0(d8, q):
+    """d8: 8 floats (one per 32-block), q: 256 ints in [-128, 127] -> 272 bytes"""
+    out = bytearray()
+    for b in range(8):
+        out += _h(d8[b]).tobytes()
+        out += np.asarray(q[32 * b:32 * b + 32], dtype=np.int8).tobytes()
+    return np.frombuffer(bytes(out), dtype=np.uint8)
+
+
+def enc_q4_k(d, dmin, sc, mn, q):
+    """sc, mn: 8 six-bit ints; q: 256 ints 0..15 -> 144 bytes (6-bit scale packing of ggml's K-quants)"""
+    s = np.zeros(12, dtype=np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    qs = np.zeros(128, dtype=np.uint8)
+    for j in range(4):  # 64-element chunk j: low nibbles elements 64j..64j+31, high nibbles 64j+32..64j+63
+        for l in range(32):
+            qs[32 * j + l] = (q[64 * j + l] & 0xF) | ((q[64 * j + 32 + l] & 0xF) << 4)
+    return np.concatenate([_h(d), _h(dmin), s, qs])
+
+
+def enc_iq4_xs(d, ls, idx):
+    """ls: 8 six-bit scales (the value is ls - 32), idx: 256 codebook indices 0..15 -> 136 bytes"""
+    sh = 0
+    sl = np.zeros(4, dtype=np.uint8)
+    for ib in range(8):
+        sl[ib // 2] |= (ls[ib] & 0xF) << (4 * (ib % 2))
+        sh |= ((ls[ib] >> 4) & 3) << (2 * ib)
+    qs = np.zeros(128, dtype=np.uint8)
+    for ib in range(8):
+        for j in range(16):
+            qs[16 * ib + j] = (idx[32 * ib + j] & 0xF) | ((idx[32 * ib + 16 + j] & 0xF) << 4)
+    return np.concatenate([_h(d), np.array([sh], dtype=np.uint16).view(np.uint8), sl, qs])
+
+
+def enc_iq3_s(d, scale_nib, gidx, sign):
+    """scale_nib: 8 four-bit scales (value 1 + 2 * nib); gidx: 64 nine-bit grid indices (one per 4 elements, in
+    element order); sign: 256 bools -> 110 bytes"""
+    qs = np.zeros(64, dtype=np.uint8)
+    qh = np.zeros(8, dtype=np.uint8)
+    signs = np.zeros(32, dtype=np.uint8)
+    sc = np.zeros(4, dtype=np.uint8)
+    for g in range(64):
+        ib, r = divmod(g, 8)
+        qs[8 * ib + r] = gidx[g] & 0xFF
+        qh[ib] |= ((gidx[g] >> 8) & 1) << r
+    for e in range(256):
+        if sign[e]:
+            signs[e // 8] |= 1 << (e % 8)
+    for ib in range(8):
+        sc[ib // 2] |= (scale_nib[ib] & 0xF) << (4 * (ib % 2))
+    return np.concatenate([_h(d), qs, qh, signs, sc])

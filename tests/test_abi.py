@@ -1,0 +1,56 @@
+"""The C ABI library without a GPU: it loads, exports every function include/qmatmul.h declares (and the binding
+describes each), and its host-only entry points answer. No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    txt = open(os.path.join(ROOT, "include", "qmatmul.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(qmatmul_\w+)\s*\(", txt)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ("qmatmul_gemv", "qmatmul_gemm", "qmatmul_moe_grouped", "qmatmul_quantize_act",
+              "qmatmul_prepare_weight", "qmatmul_release_weight"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(qm):
+    lib = qm.load_library()
+    for n in declared_functions():
+        assert hasattr(lib, n), n
+    bound = {s[0] for s in qm.SIGNATURES}
+    assert bound == set(declared_functions())
+
+
+def test_host_only_entry_points(qm):
+    lib = qm.load_library()
+    assert lib.qmatmul_sb_bytes(8) == 272 and lib.qmatmul_sb_bytes(12) == 144
+    assert lib.qmatmul_sb_bytes(21) == 110 and lib.qmatmul_sb_bytes(23) == 136 and lib.qmatmul_sb_bytes(2) == 0
+    assert lib.qmatmul_weight_bytes(23, 17408, 5120) >= 17408 * 20 * 136
+    assert lib.qmatmul_weight_bytes(23, 16, 100) == 0
+    assert lib.qmatmul_moe_workspace_size(4096, 256, 8, 2048, 512) > 32768 * 2048 * 4
+    L = qm.moe_ws_layout(4096, 256, 8, 2048, 512)
+    assert L.slots == 32768 and L.max_tiles == 32768 // L.tile_rows + 256 and L.total >= L.y + 32768 * 2048 * 4
+
+
+def test_argument_errors_need_no_gpu(qm):
+    lib = qm.load_library()
+    h = ctypes.c_void_p()
+    # null source pointer / unsupported type / bad K: rejected before any device call
+    assert lib.qmatmul_prepare_weight(23, None, 1, 16, 256, None, ctypes.byref(h)) == 1
+    assert b"null" in lib.qmatmul_last_error()
+    buf = (ctypes.c_uint8 * 16)()
+    assert lib.qmatmul_prepare_weight(2, buf, 0, 16, 256, None, ctypes.byref(h)) == 3
+    assert lib.qmatmul_prepare_weight(23, buf, 0, 16, 100, None, ctypes.byref(h)) == 2
+    assert lib.qmatmul_gemv(None, None, None, None, 1, 1, None, 0, 0, 0, None) == 1
+    assert lib.qmatmul_quantize_act(buf, 32, 1, 1, 33, buf, buf, buf, None) == 2
+    with pytest.raises(qm.QMatmulError):
+        qm._call("qmatmul_moe_ws_layout", 0, 1, 1, 1, 1, None)

@@ -1,0 +1,236 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle on the same seeded inputs.
+
+Bars: quantized activations and int32 block sums bit-exact; f32 outputs within 1e-4 of the
+oracle's int8 path and within 1e-3 of the f32 dequantized reference, both as max |err| / max |ref| over the output.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from arcinfer_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+
+TOL_INT8_PATH = 1e-4
+TOL_F32_REF = 1e-3
+TYPES = [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S]
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def acts(qm, x, dev, M_stride=None):
+    import torch
+    xt = to_dev(x.astype(np.float32), dev)
+    aq, asc, absum = qm.quantize_act(xt, M_stride=M_stride)
+    torch.cuda.synchronize()
+    return aq, asc, absum
+
+
+# ---- (a) activation quantizer
+@pytest.mark.parametrize("M,Ms,K", [(1, 16, 4096), (7, 16, 512), (64, 64, 5120), (3, 3, 17408)])
+def test_quantizer_bit_exact(qm, dev, M, Ms, K):
+    rng = np.random.default_rng(M * 1000 + K)
+    x = rng.standard_normal((M, K)).astype(np.float32) * rng.choice([1.0, 30.0, 1e-3], size=(M, K)).astype(np.float32)
+    x[0, :32] = 0.0  # a zero block
+    x[0, 32:64] = np.float32(0.5) * np.arange(32, dtype=np.float32)  # ties at amax 15.5? (q = 127 * v / 15.5)
+    if K >= 128:
+        x[0, 64:96] = np.array([127.0, 0.5, 1.5, 2.5, -0.5, -1.5] + [3.5] * 26, dtype=np.float32)  # exact ties
+    aq, asc, absum = acts(qm, x, dev, Ms)
+    raq, rasc, rabs = oracle.quantize_act(x, M_stride=Ms)
+    assert np.array_equal(aq.cpu().numpy(), raq)
+    assert np.array_equal(asc.cpu().numpy().view(np.uint32), rasc.view(np.uint32))
+    assert np.array_equal(absum.cpu().numpy(), rabs)
+
+
+def test_quantizer_strided_input(qm, dev):
+    import torch
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 1024)).astype(np.float32)
+    xt = to_dev(x, dev)[:, :512]  # ldx 1024, K 512
+    aq, asc, absum = qm.quantize_act(xt, M_stride=8)
+    torch.cuda.synchronize()
+    raq, rasc, rabs = oracle.quantize_act(np.ascontiguousarray(x[:, :512]), M_stride=8)
+    assert np.array_equal(aq.cpu().numpy(), raq) and np.array_equal(absum.cpu().numpy(), rabs)
+    assert np.array_equal(asc.cpu().numpy(), rasc)
+
+
+# ---- (b) decode GEMV
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (48, 768, 3), (40, 8192, 1), (16, 256, 8)])
+def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
+    rng = np.random.default_rng(qtype + N + K)
+    W = F.synth_weight(qtype, N, K, seed=qtype * 7 + K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    aq, asc, absum = acts(qm, x, dev, M_stride=max(T, 16))
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    isum, msum = qm.gemv_blocksums(w, aq, absum, T=T)
+    _, risum, rmsum = oracle.blockdot(qtype, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=T,
+                                      blocksums=True)
+    assert np.array_equal(isum.cpu().numpy(), risum)
+    if qtype == F.Q4_K:
+        assert np.array_equal(msum.cpu().numpy(), rmsum)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (200, 2048, 1), (72, 17408, 1), (96, 5120, 2), (64, 1536, 5)])
+def test_gemv_f32_parity(qm, dev, qtype, N, K, T):
+    import torch
+    rng = np.random.default_rng(qtype * 3 + N)
+    W = F.synth_weight(qtype, N, K, seed=qtype + 11 * N)
+    x = F.synth_activations(T, K, seed=N + K, outlier_frac=0.01)
+    aq, asc, absum = acts(qm, x, dev, M_stride=16)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    C = qm.gemv(w, aq, asc, absum, T=T)
+    torch.cuda.synchronize()
+    naq, nasc, nabs = aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy()
+    ref = oracle.blockdot(qtype, W, K, naq, nasc, nabs, M=T)
+    assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+    xq = naq[:T].astype(np.float32) * np.repeat(nasc[:, :T].T, 32, axis=1)
+    ref32 = oracle.matmul_f32(qtype, W, K, xq)
+    assert rel_err(C.cpu().numpy(), ref32) < TOL_F32_REF
+
+
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.IQ4_XS])
+def test_gemv_accumulate_offset_and_tokens(qm, dev, qtype):
+    import torch
+    N, K = 128, 2048
+    W = F.synth_weight(qtype, N, K, seed=9)
+    x = F.synth_activations(4, K, seed=10)
+    aq, asc, absum = acts(qm, x, dev, M_stride=16)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    one = [qm.gemv(w, aq[t:t + 1].contiguous(), asc[:, t:t + 1].contiguous(), absum[:, t:t + 1].contiguous(), T=1)
+           for t in range(4)]
+    multi = qm.gemv(w, aq, asc, absum, T=4)
+    torch.cuda.synchronize()
+    for t in range(4):  # same lanes, same order per token: bit-identical
+        assert torch.equal(one[t][0], multi[t])
+    C = torch.full((4, 3 * N), 2.0, device=dev)
+    qm.gemv(w, aq, asc, absum, T=4, C=C, ldc=3 * N, c_off=N, accumulate=1)
+    torch.cuda.synchronize()
+    assert torch.equal(C[:, N:2 * N], multi + 2.0)
+    assert torch.all(C[:, :N] == 2.0) and torch.all(C[:, 2 * N:] == 2.0)
+
+
+def test_gemv_baseline_q8_0_4096(qm, dev):
+    """Q8_0 4096 x 4096, seed 0."""
+    import torch
+    N = K = 4096
+    W = F.synth_weight(F.Q8_0, N, K, seed=0)
+    x = F.synth_activations(1, K, seed=0)
+    aq, asc, absum = acts(qm, x, dev, M_stride=16)
+    w = qm.QWeight(F.Q8_0, to_dev(W, dev), N, K)
+    C = qm.gemv(w, aq, asc, absum)
+    torch.cuda.synchronize()
+    ref = oracle.blockdot(F.Q8_0, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=1)
+    assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+def test_gemv_baseline_iq4_xs(qm, dev, N, K):
+    """BASELINE config 1 (north star shapes), full size."""
+    import torch
+    W = F.synth_weight(F.IQ4_XS, N, K, seed=1)
+    x = F.synth_activations(1, K, seed=1)
+    aq, asc, absum = acts(qm, x, dev, M_stride=16)
+    w = qm.QWeight(F.IQ4_XS, to_dev(W, dev), N, K)
+    C = qm.gemv(w, aq, asc, absum)
+    torch.cuda.synchronize()
+    ref = oracle.blockdot(F.IQ4_XS, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=1)
+    assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+
+
+# ---- (c) prompt GEMM on int8 MFMA
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("M,N,K", [(32, 128, 512), (37, 144, 768)])
+def test_gemm_blocksums_bit_exact(qm, dev, qtype, M, N, K):
+    rng = np.random.default_rng(M + N + qtype)
+    W = F.synth_weight(qtype, N, K, seed=qtype * 5 + M)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    aq, asc, absum = acts(qm, x, dev, M_stride=M)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    isum = qm.gemm_blocksums(w, aq)
+    _, risum, _ = oracle.blockdot(qtype, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(),
+                                  blocksums=True)
+    assert np.array_equal(isum.cpu().numpy(), risum)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("M,Ms,N,K", [(64, 64, 256, 1024), (100, 128, 384, 2048), (16, 16, 128, 256),
+                                      (130, 130, 512, 5120)])
+def test_gemm_f32_parity(qm, dev, qtype, M, Ms, N, K):
+    import torch
+    W = F.synth_weight(qtype, N, K, seed=qtype + M + N)
+    x = F.synth_activations(M, K, seed=M * 3 + K, outlier_frac=0.01)
+    aq, asc, absum = acts(qm, x, dev, M_stride=Ms)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    C = qm.gemm(w, aq, asc, absum, M=M)
+    torch.cuda.synchronize()
+    naq, nasc, nabs = aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy()
+    ref = oracle.blockdot(qtype, W, K, naq, nasc, nabs, M=M)
+    assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+    xq = naq[:M].astype(np.float32) * np.repeat(nasc[:, :M].T, 32, axis=1)
+    assert rel_err(C.cpu().numpy(), oracle.matmul_f32(qtype, W, K, xq)) < TOL_F32_REF
+
+
+def test_gemm_accumulate_modes(qm, dev):
+    import torch
+    M, N, K = 64, 256, 1024
+    W = F.synth_weight(F.IQ4_XS, N, K, seed=3)
+    x = F.synth_activations(M, K, seed=4)
+    aq, asc, absum = acts(qm, x, dev)
+    w = qm.QWeight(F.IQ4_XS, to_dev(W, dev), N, K)
+    base = qm.gemm(w, aq, asc, absum)
+    C = torch.randn(M, 2 * N + 16, device=dev)
+    C0 = C.clone()
+    qm.gemm(w, aq, asc, absum, C=C, ldc=2 * N + 16, c_off=N, accumulate=1)
+    torch.cuda.synchronize()
+    assert torch.equal(C[:, N:2 * N], C0[:, N:2 * N] + base)
+    assert torch.equal(C[:, :N], C0[:, :N]) and torch.equal(C[:, 2 * N:], C0[:, 2 * N:])
+    G = torch.randn(M, N, device=dev)
+    S = G.clone()
+    qm.gemm(w, aq, asc, absum, C=S, ldc=N, accumulate=2)
+    torch.cuda.synchronize()
+    ref = (G.double() / (1 + torch.exp(-G.double()))) * base.double()
+    assert torch.max(torch.abs(S.double() - ref)) / torch.max(torch.abs(ref)) < 1e-6
+
+
+def test_gemm_baseline_q4_k_2k_sampled(qm, dev):
+    """BASELINE config 2 at full size: M 2048, K 5120, N 17408; every 64th output column against the oracle."""
+    import torch
+    M, N, K = 2048, 17408, 5120
+    W = F.synth_weight(F.Q4_K, N, K, seed=2)
+    x = F.synth_activations(M, K, seed=2, outlier_frac=0.01, outlier_scale=20.0)
+    aq, asc, absum = acts(qm, x, dev)
+    w = qm.QWeight(F.Q4_K, to_dev(W, dev), N, K)
+    C = qm.gemm(w, aq, asc, absum)
+    torch.cuda.synchronize()
+    Cn = C.cpu().numpy()
+    ref = oracle.blockdot(F.Q4_K, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), col_stride=64)
+    assert rel_err(Cn[:, ::64], ref[:, ::64]) < TOL_INT8_PATH
+    assert np.all(np.isfinite(Cn))
+
+
+@pytest.mark.parametrize("M", [1, 512])
+def test_iq3_s_baseline_5120(qm, dev, M):
+    """IQ3_S 5120 x 5120 at M = 1 (GEMV) and M = 512 (GEMM, every 16th column checked)."""
+    import torch
+    N = K = 5120
+    W = F.synth_weight(F.IQ3_S, N, K, seed=3)
+    x = F.synth_activations(M, K, seed=3)
+    aq, asc, absum = acts(qm, x, dev, M_stride=max(M, 16))
+    w = qm.QWeight(F.IQ3_S, to_dev(W, dev), N, K)
+    C = qm.gemv(w, aq, asc, absum) if M == 1 else qm.gemm(w, aq, asc, absum, M=M)
+    torch.cuda.synchronize()
+    stride = 1 if M == 1 else 16
+    ref = oracle.blockdot(F.IQ3_S, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=M,
+                          col_stride=stride)
+    assert rel_err(C.cpu().numpy()[:, ::stride], ref[:, ::stride]) < TOL_INT8_PATH

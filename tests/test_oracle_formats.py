@@ -1,0 +1,142 @@
+"""Pins the oracle's format code (oracle/qref.c) without retyping it:
+  - fp16 conversions against numpy's IEEE half (exhaustive for half -> float);
+  - the codebooks against published ggml values and structural invariants;
+  - each block decoder against an independent encoder (tests/encoders.py, written from the GGML block structs):
+    chosen fields must come back exactly, and the dequantized values must equal the field formula;
+  - closed forms: a block whose nibbles are all i dequantizes to d * sc * kvalues[i], zero scales give zeros.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from arcinfer_amd import formats as F
+from tests import encoders as enc
+
+KV_PUBLISHED = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def test_fp16_to_f32_exhaustive():
+    h = np.arange(65536, dtype=np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = oracle.fp16_to_f32(h)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_fp16_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * np.float32(10.0) ** rng.integers(-8, 5, 4000),
+        # exact half-way cases between adjacent halves (ties go to even), normal and subnormal
+        ((np.arange(1, 400, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10)),
+        ((np.arange(1, 400, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24)),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 6e-8, 3e-8, 2.98e-8], dtype=np.float32),
+    ]).astype(np.float32)
+    ref = x.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_fp16(x)
+    assert np.array_equal(got, ref)
+
+
+def test_codebooks_match_published_and_invariants():
+    import re
+    txt = open(oracle.HERE + "/iq_tables.inc").read()
+    kv = [int(v) for v in re.search(r"QM_IQ4NL_VALUES_INIT \{([^}]*)\}", txt).group(1).split(",")]
+    assert kv == KV_PUBLISHED
+    grid = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt)]
+    assert len(grid) == 512
+    assert grid[0] == 0x01010101 and grid[1] == 0x01010103 and grid[-1] == 0x0F0F0101  # published end entries
+    assert grid == sorted(grid) and len(set(grid)) == 512  # ggml's IQ3_S grid is sorted and distinct
+    for g in grid:
+        for j in range(4):
+            b = (g >> (8 * j)) & 0xFF
+            assert b % 2 == 1 and 1 <= b <= 15  # IQ3_S grid values are odd magnitudes 1..15
+    # the product's copy is the same data
+    prod = open(oracle.HERE + "/../arcinfer_amd/csrc/iq_tables.inc").read()
+    assert prod == txt
+
+
+def _kv():
+    return np.array(KV_PUBLISHED, dtype=np.int64)
+
+
+def test_q8_0_decoder_round_trip():
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        d8 = rng.standard_normal(8).astype(np.float16).astype(np.float32)
+        q = rng.integers(-128, 128, 256)
+        o = oracle.decode_sb(F.Q8_0, enc.enc_q8_0(d8, q))
+        assert np.array_equal(o["q"], q) and np.array_equal(o["d8"], d8)
+        w = oracle.dequant_rows(F.Q8_0, enc.enc_q8_0(d8, q)[None], 256)[0]
+        assert np.array_equal(w, (np.repeat(d8, 32) * q.astype(np.float32)).astype(np.float32))
+
+
+def test_q4_k_decoder_round_trip():
+    rng = np.random.default_rng(2)
+    for _ in range(50):
+        d, dmin = np.float16(rng.random()), np.float16(rng.random())
+        sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        q = rng.integers(0, 16, 256)
+        raw = enc.enc_q4_k(d, dmin, sc, mn, q)
+        o = oracle.decode_sb(F.Q4_K, raw)
+        assert np.array_equal(o["sc"], sc) and np.array_equal(o["mn"], mn) and np.array_equal(o["q"], q)
+        assert o["d"] == np.float32(d) and o["dmin"] == np.float32(dmin)
+        w = oracle.dequant_rows(F.Q4_K, raw[None], 256)[0]
+        e = np.arange(256) // 32
+        ref = (np.float32(d) * sc[e].astype(np.float32) * q.astype(np.float32)
+               - np.float32(dmin) * mn[e].astype(np.float32)).astype(np.float32)
+        assert np.array_equal(w, ref)
+
+
+def test_iq4_xs_decoder_round_trip_and_closed_form():
+    rng = np.random.default_rng(3)
+    kv = _kv()
+    for _ in range(50):
+        d = np.float16(rng.standard_normal())
+        ls, idx = rng.integers(0, 64, 8), rng.integers(0, 16, 256)
+        raw = enc.enc_iq4_xs(d, ls, idx)
+        o = oracle.decode_sb(F.IQ4_XS, raw)
+        assert np.array_equal(o["sc"], ls - 32) and np.array_equal(o["q"], kv[idx])
+    # closed form: every nibble i, every scale 33 (sc 1), d 1 -> the codebook itself
+    for i in range(16):
+        raw = enc.enc_iq4_xs(np.float16(1.0), [33] * 8, [i] * 256)
+        assert np.all(oracle.dequant_rows(F.IQ4_XS, raw[None], 256)[0] == KV_PUBLISHED[i])
+    # ls = 32 -> scale 0 -> all zeros
+    raw = enc.enc_iq4_xs(np.float16(3.0), [32] * 8, rng.integers(0, 16, 256))
+    assert np.all(oracle.dequant_rows(F.IQ4_XS, raw[None], 256)[0] == 0)
+
+
+def test_iq3_s_decoder_round_trip():
+    import re
+    txt = open(oracle.HERE + "/iq_tables.inc").read()
+    grid = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt)], dtype=np.int64)
+    rng = np.random.default_rng(4)
+    for it in range(50):
+        d = np.float16(rng.random())
+        nib = rng.integers(0, 16, 8)
+        gidx = rng.integers(0, 512, 64)
+        if it == 0:
+            gidx[:] = 256 + np.arange(64)  # the 9th index bit set everywhere
+        sign = rng.random(256) < 0.5
+        if it == 1:
+            sign[:] = True
+        raw = enc.enc_iq3_s(d, nib, gidx, sign)
+        o = oracle.decode_sb(F.IQ3_S, raw)
+        mag = np.array([(grid[gidx[e // 4]] >> (8 * (e % 4))) & 0xFF for e in range(256)])
+        assert np.array_equal(o["q"], np.where(sign, -mag, mag))
+        assert np.array_equal(o["sc"], 1 + 2 * nib)
+        w = oracle.dequant_rows(F.IQ3_S, raw[None], 256)[0]
+        ref = (np.float32(d) * (1 + 2 * nib[np.arange(256) // 32]).astype(np.float32)
+               * np.where(sign, -mag, mag).astype(np.float32)).astype(np.float32)
+        assert np.array_equal(w, ref)
+
+
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S])
+def test_synth_weights_have_the_requested_statistics(qtype):
+    W = F.synth_weight(qtype, 64, 512, seed=5)
+    assert W.shape == (64, F.row_bytes(qtype, 512))
+    w = oracle.dequant_rows(qtype, W, 512)
+    assert np.all(np.isfinite(w))
+    if qtype == F.Q8_0:
+        q = W.reshape(-1, 34)[:, 2:].view(np.int8)
+        assert q.min() >= -127 and q.max() <= 127
