@@ -1,0 +1,229 @@
+"""Benchmark of the quantized matmul path on one MI355X (prints ONE JSON line).
+
+Metric: IQ4_XS GEMV weight GB/s (decode) + int8 GEMM TOPS (2K prompt), % of peak.
+  value     -- IQ4_XS decode GEMV weight GB/s. A step is one decode pass over the two 27B-class FFN matrices,
+               K=5120 -> N=17408 (gate/up) and K=17408 -> N=5120 (down), batch 1, weights resident in HBM and
+               rotated over 8 distinct copies of each matrix (758 MB > the 256 MB Infinity Cache).
+  gemm      -- the 2K-token prompt GEMM: Q4_K weights K=5120, N=17408, M=2048 int8 activations, int8 MFMA;
+               TOPS = 2*M*N*K / time.
+  moe       -- the MoE FFN (256 experts, E 2048, F 512, T 4096, top-8, Zipf 1.1 router, IQ4_XS), reported.
+  roofline  -- for each kernel: algorithmic bytes (or int8 ops) per launch / average launch time, measured with
+               HIP events on the launch stream, against MI355X peaks (HBM 8 TB/s, dense int8 MFMA 5.0 POPS).
+  cpu_baseline -- the repository's C restatement of the reference CPU path (oracle/), timed on this host.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "IQ4_XS GEMV weight GB/s (decode) + int8 GEMM TOPS (2K prompt), % of peak"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--only", choices=["all", "gemv", "gemm", "moe"], default="all")
+    p.add_argument("--copies", type=int, default=8)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU work budget per baseline leg")
+    p.add_argument("--profile", action="store_true",
+                   help="short run for rocprofv3: a few launches of each kernel plus a 1 GiB copy for calibration")
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup, stream):
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall
+
+
+def profile_traffic(kernel_key):
+    """Bytes per launch from the committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, calibrated on a copy
+    kernel), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"^TRAFFIC\s+(\S+)\s+bytes_per_launch=(\d+)", line)
+        if m and m.group(1) == kernel_key:
+            return int(m.group(2))
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the multi-GPU design is "
+              "described in DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from arcinfer_amd import formats as F
+    from arcinfer_amd import qmatmul as qm
+
+    qm.load_library()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    out = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+           "data": "synthetic (seeded GGUF-format weights, N(0,1) activations; BASELINE.json configs)",
+           "config": {"workload": "IQ4_XS decode GEMV, batch 1: K=5120->N=17408 and K=17408->N=5120 per step, "
+                                  f"{args.copies} rotating weight copies each", "parallelism": "none (1 GPU)"}}
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    if args.profile:
+        args.steps, args.warmup, args.copies = 4, 1, 2
+
+    # ---------------- IQ4_XS decode GEMV (north star)
+    if args.only in ("all", "gemv"):
+        shapes = [(17408, 5120), (5120, 17408)]
+        mats = []
+        for si, (N, K) in enumerate(shapes):
+            W = F.synth_weight(F.IQ4_XS, N, K, seed=1 + si)
+            Wd = torch.from_numpy(W).to(dev)
+            copies = [qm.QWeight(F.IQ4_XS, Wd, N, K) for _ in range(args.copies)]
+            del Wd
+            x = torch.from_numpy(F.synth_activations(1, K, seed=1 + si)).to(dev)
+            aq, asc, absum = qm.quantize_act(x, M_stride=16)
+            C = torch.empty((1, N), device=dev)
+            mats.append((N, K, W, copies, aq, asc, absum, C))
+        torch.cuda.synchronize()
+        bytes_per_step = sum(F.weight_bytes(F.IQ4_XS, N, K) for N, K, *_ in mats)
+
+        def step(i):
+            for N, K, W, copies, aq, asc, absum, C in mats:
+                qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N)
+
+        ms, wall = timed(step, args.steps, args.warmup, stream)
+        gbs = bytes_per_step / (ms * 1e-3) / 1e9
+        out["value"] = round(gbs, 1)
+        out["ms_per_step"] = round(ms, 5)
+        # per-matrix launch times (each kernel alone, same rotation)
+        per = {}
+        for N, K, W, copies, aq, asc, absum, C in mats:
+            def one(i, copies=copies, aq=aq, asc=asc, absum=absum, C=C, N=N):
+                qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N)
+            ms1, _ = timed(one, args.steps, args.warmup, stream)
+            b = F.weight_bytes(F.IQ4_XS, N, K)
+            per[f"{K}->{N}"] = {"us_per_launch": round(ms1 * 1e3, 2), "GB/s": round(b / (ms1 * 1e-3) / 1e9, 1),
+                               "weight_bytes": b}
+        out["gemv_per_matrix"] = per
+        # dominant kernel: the gate/up matrix (K 5120 -> N 17408)
+        gu = per["5120->17408"]
+        traffic = profile_traffic("gemv_iq4_xs_5120x17408")
+        out["roofline"] = {"bound": "hbm", "kernel": "gemv_kernel<IQ4_XS> K=5120 N=17408",
+                           "achieved": gu["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(gu["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                           "algorithmic_bytes_per_launch": gu["weight_bytes"]}
+        out["gemv_frac_of_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 4)
+        if not args.no_cpu and not args.profile:
+            import oracle
+            N, K, W, copies, aq, asc, absum, C = mats[0]
+            naq, nasc, nabs = aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy()
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                oracle.blockdot(F.IQ4_XS, W, K, naq, nasc, nabs, M=1, nthreads=nthreads)
+                reps += 1
+            cpu_s = (time.perf_counter() - t0) / reps
+            out["cpu_baseline"] = {"value": round(F.weight_bytes(F.IQ4_XS, N, K) / cpu_s / 1e9, 3), "unit": "GB/s",
+                                   "cores": nthreads, "kind": "port",
+                                   "sample": f"IQ4_XS K=5120 N=17408 int8 block-dot GEMV (oracle/qref.c, -O3, "
+                                             f"OpenMP), {reps} full passes in {reps * cpu_s:.1f} s"}
+        for m in mats:
+            for c in m[3]:
+                c.release()
+        del mats
+        torch.cuda.empty_cache()
+
+    # ---------------- Q4_K prompt GEMM, 2048 tokens
+    if args.only in ("all", "gemm"):
+        M, N, K = 2048, 17408, 5120
+        W = F.synth_weight(F.Q4_K, N, K, seed=2)
+        w = qm.QWeight(F.Q4_K, torch.from_numpy(W).to(dev), N, K)
+        x = torch.from_numpy(F.synth_activations(M, K, seed=2, outlier_frac=0.01, outlier_scale=20.0)).to(dev)
+        aq, asc, absum = qm.quantize_act(x)
+        C = torch.empty((M, N), device=dev)
+        steps = max(2, args.steps // 5)
+        ms, _ = timed(lambda i: qm.gemm(w, aq, asc, absum, C=C, ldc=N), steps, args.warmup, stream)
+        ops = 2.0 * M * N * K
+        tops = ops / (ms * 1e-3) / 1e12
+        g = {"value": round(tops, 1), "unit": "TOPS", "ms_per_launch": round(ms, 4),
+             "config": "Q4_K K=5120 N=17408, M=2048 (1% outlier channels x20), int8 per-32 activations",
+             "roofline": {"bound": "mfma", "kernel": "gemm_kernel<Q4_K> dense", "achieved": round(tops, 1),
+                          "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                          "traffic": profile_traffic("gemm_q4_k_2048x5120x17408"),
+                          "algorithmic_ops_per_launch": int(ops)}}
+        # activation quantizer for the same 2048 x 5120 input (the step before the GEMM)
+        msq, _ = timed(lambda i: qm.quantize_act(x), steps, 1, stream)
+        g["quantize_us"] = round(msq * 1e3, 2)
+        if not args.no_cpu and not args.profile:
+            import oracle
+            naq, nasc, nabs = aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy()
+            stride = 64
+            t0 = time.perf_counter()
+            oracle.blockdot(F.Q4_K, W, K, naq, nasc, nabs, col_stride=stride, nthreads=nthreads)
+            cpu_s = (time.perf_counter() - t0) * stride
+            g["cpu_baseline"] = {"value": round(ops / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthreads,
+                                 "kind": "port", "sample": f"every {stride}th output column of the same GEMM "
+                                                           f"(oracle/qref.c int8 block-dot), time x {stride}"}
+        out["gemm"] = g
+        w.release()
+        del C, x, aq, asc, absum
+        torch.cuda.empty_cache()
+
+    # ---------------- MoE FFN (reported)
+    if args.only in ("all", "moe"):
+        NE, E, Fd, T, NU = 256, 2048, 512, 4096, 8
+        ws_ = []
+        for i, (rows, K) in enumerate(((NE * Fd, E), (NE * Fd, E), (NE * E, Fd))):
+            W = F.synth_weight(F.IQ4_XS, rows, K, seed=40 + i, sigma=0.05)
+            ws_.append(qm.QWeight(F.IQ4_XS, torch.from_numpy(W).to(dev), rows, K))
+            del W
+        x = torch.from_numpy(F.synth_activations(T, E, seed=43)).to(dev)
+        aq, asc, absum = qm.quantize_act(x)
+        lg = torch.from_numpy(F.zipf_router_logits(T, NE, seed=44)).to(dev)
+        wsp = qm.moe_workspace(T, NE, NU, E, Fd, device=dev)
+        xo = torch.empty((T, E), device=dev)
+        steps = max(2, args.steps // 5)
+        ms, _ = timed(lambda i: qm.moe_grouped(ws_[0], ws_[1], ws_[2], NE, lg, NU, aq, asc, xo, wsp), steps,
+                      args.warmup, stream)
+        ops = 2.0 * T * NU * (2 * Fd * E + E * Fd)
+        wbytes = 3 * F.weight_bytes(F.IQ4_XS, NE * Fd, E)
+        out["moe"] = {"ms_per_launch": round(ms, 4), "TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
+                      "expert_weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                      "config": "256 experts IQ4_XS, E 2048, F 512, T 4096, top-8, Zipf(1.1) router; "
+                                "route + scan + scatter + gate/up + down + combine"}
+        for w_ in ws_:
+            w_.release()
+
+    if args.profile:
+        # calibration copy for the FETCH_SIZE / WRITE_SIZE counters: 1 GiB read + 1 GiB written
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(2):
+            b.copy_(a)
+        torch.cuda.synchronize()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
