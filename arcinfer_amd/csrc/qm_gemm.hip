@@ -13,18 +13,22 @@
 //     accumulators); the f32 epilogue applies activation scale x weight scale per block
 //     (zero/kernels/gemm.cl:367-412 applies the same per-32 scales), and Q4_K's min term from the per-32 sums.
 // The 32x32 MFMA result layout: lane l holds column j = l % 32 and rows 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+#include <stdlib.h>
+
 #include "qm_launch.h"
 
 namespace qm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int A_STRIDE = 272;  // LDS bytes per staged activation row
 
 template <int TYPE, int MT> struct GemmLds {
-  uint8_t a[32 * MT * A_STRIDE];
-  float asc[8 * 32 * MT];
+  alignas(16) uint8_t a[32 * MT * A_STRIDE];
+  alignas(16) float asc[8 * 32 * MT];
   float u[Traits<TYPE>::MINS ? 8 * 32 * MT : 1];
   int arow[32 * MT];
   typename std::conditional<TYPE == T_IQ3_S, Iq3Lds, int>::type iq3;
@@ -42,14 +46,64 @@ __device__ __forceinline__ void iq3s_pair_rt(const Iq3Lds* t, uint32_t q0, uint3
   w1 = (t->grid[i2] ^ m.y) + m.w;
 }
 
-// Per-superblock weight scales of row n: dsc[b] = d * sc_b (Q8_0: the block's f16 scale), dmn[b] = dmin * mn_b;
-// isc[b] = the integer scale (for the block-sum hook).
+// A lane's payload of one 32-block (the bytes its k-half needs): 16 B for Q8_0 (its half of the 32 int8), the block's
+// 16 nibble bytes for Q4_K / IQ4_XS, the 8 index bytes + 4 sign bytes for IQ3_S (.w unused).
 template <int TYPE>
-__device__ __forceinline__ void sb_scales(const WView& w, int n, int s, float dsc[8], float dmn[8], int isc[8]) {
+__device__ __forceinline__ uint4 load_payload(const WView& w, int n, int blk, int hf) {
   using Tr = Traits<TYPE>;
-  const uint8_t* hp = w.hdr + ((size_t)n * (w.K / 256) + s) * Tr::HB;
+  const uint8_t* qp = w.qs + ((size_t)n * (w.K / 32) + blk) * Tr::QB;
   if constexpr (TYPE == T_Q8_0) {
-    const uint4 h = *(const uint4*)hp;
+    return *(const uint4*)(qp + 16 * hf);
+  } else if constexpr (TYPE == T_IQ3_S) {
+    const uint32_t* q = (const uint32_t*)qp;
+    return make_uint4(q[0], q[1], q[2], 0u);
+  } else {
+    return *(const uint4*)qp;
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ uint4 load_header(const WView& w, int n, int s) {
+  const uint8_t* hp = w.hdr + ((size_t)n * (w.K / 256) + s) * Traits<TYPE>::HB;
+  if constexpr (TYPE == T_IQ4_XS) {
+    const uint2 h = *(const uint2*)hp;
+    return make_uint4(h.x, h.y, 0u, 0u);
+  } else {
+    return *(const uint4*)hp;
+  }
+}
+
+// The MFMA B operand (16 int8 weights of k-half hf) from a lane's payload of 32-block b of its superblock.
+template <int TYPE>
+__device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, const KvTab& kv, const Iq3Lds* iq3) {
+  v4i r;
+  if constexpr (TYPE == T_Q8_0) {
+    r[0] = (int)q.x; r[1] = (int)q.y; r[2] = (int)q.z; r[3] = (int)q.w;
+  } else if constexpr (TYPE == T_Q4_K || TYPE == T_IQ4_XS) {
+    const int sh = 4 * hf;
+    const uint32_t x0 = q.x >> sh, x1 = q.y >> sh, x2 = q.z >> sh, x3 = q.w >> sh;
+    if constexpr (TYPE == T_Q4_K) {
+      r[0] = (int)(x0 & 0x0F0F0F0Fu); r[1] = (int)(x1 & 0x0F0F0F0Fu);
+      r[2] = (int)(x2 & 0x0F0F0F0Fu); r[3] = (int)(x3 & 0x0F0F0F0Fu);
+    } else {
+      r[0] = (int)kv_lookup4(kv, x0); r[1] = (int)kv_lookup4(kv, x1);
+      r[2] = (int)kv_lookup4(kv, x2); r[3] = (int)kv_lookup4(kv, x3);
+    }
+  } else {
+    const uint32_t qh = ((b < 4 ? hdr.x : hdr.y) >> (8 * (b & 3))) & 0xFFu;
+    uint32_t w0, w1, w2, w3;
+    iq3s_pair_rt(iq3, q.x, q.y, qh, q.z, 2 * hf, w0, w1);
+    iq3s_pair_rt(iq3, q.x, q.y, qh, q.z, 2 * hf + 1, w2, w3);
+    r[0] = (int)w0; r[1] = (int)w1; r[2] = (int)w2; r[3] = (int)w3;
+  }
+  return r;
+}
+
+// Per-block weight scales of one superblock from its header: dsc[b] = d * sc_b (Q8_0: the block's f16 scale),
+// dmn[b] = dmin * mn_b (Q4_K), isc[b] = the integer scale.
+template <int TYPE>
+__device__ __forceinline__ void sb_scales(uint4 h, float dsc[8], float dmn[8], int isc[8]) {
+  if constexpr (TYPE == T_Q8_0) {
     const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -58,7 +112,6 @@ __device__ __forceinline__ void sb_scales(const WView& w, int n, int s, float ds
       isc[b] = 1;
     }
   } else if constexpr (TYPE == T_Q4_K) {
-    const uint4 h = *(const uint4*)hp;
     const float d = h2f(h.x), dmin = h2f(h.x >> 16);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -69,7 +122,6 @@ __device__ __forceinline__ void sb_scales(const WView& w, int n, int s, float ds
       isc[b] = sc;
     }
   } else if constexpr (TYPE == T_IQ4_XS) {
-    const uint2 h = *(const uint2*)hp;
     const float d = h2f(h.x);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -78,7 +130,6 @@ __device__ __forceinline__ void sb_scales(const WView& w, int n, int s, float ds
       dmn[b] = 0.0f;
     }
   } else {
-    const uint4 h = *(const uint4*)hp;
     const float d = h2f(h.w);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -89,53 +140,34 @@ __device__ __forceinline__ void sb_scales(const WView& w, int n, int s, float ds
   }
 }
 
-// The MFMA B operand of row n, 32-block blk, k-half hf: 16 int8 weights.
-template <int TYPE>
-__device__ __forceinline__ v4i b_operand(const WView& w, const Iq3Lds* iq3, const KvTab& kv, int n, int blk, int hf,
-                                         int s) {
-  using Tr = Traits<TYPE>;
-  const int nb = w.K / 32;
-  const uint8_t* qp = w.qs + ((size_t)n * nb + blk) * Tr::QB;
-  v4i r;
-  if constexpr (TYPE == T_Q8_0) {
-    const uint4 q = *(const uint4*)(qp + 16 * hf);
-    r[0] = (int)q.x; r[1] = (int)q.y; r[2] = (int)q.z; r[3] = (int)q.w;
-  } else if constexpr (TYPE == T_Q4_K || TYPE == T_IQ4_XS) {
-    const uint4 q = *(const uint4*)qp;
-    const int sh = 4 * hf;
-    uint32_t x0 = q.x >> sh, x1 = q.y >> sh, x2 = q.z >> sh, x3 = q.w >> sh;
-    if constexpr (TYPE == T_Q4_K) {
-      r[0] = (int)(x0 & 0x0F0F0F0Fu); r[1] = (int)(x1 & 0x0F0F0F0Fu);
-      r[2] = (int)(x2 & 0x0F0F0F0Fu); r[3] = (int)(x3 & 0x0F0F0F0Fu);
-    } else {
-      r[0] = (int)kv_lookup4(kv, x0); r[1] = (int)kv_lookup4(kv, x1);
-      r[2] = (int)kv_lookup4(kv, x2); r[3] = (int)kv_lookup4(kv, x3);
-    }
-  } else {
-    const uint32_t* qw = (const uint32_t*)qp;
-    const uint32_t q0 = qw[0], q1 = qw[1], sg = qw[2];
-    const uint8_t* hp = w.hdr + ((size_t)n * (w.K / 256) + s) * Tr::HB;
-    const uint32_t qh = hp[blk & 7];
-    uint32_t w0, w1, w2, w3;
-    iq3s_pair_rt(iq3, q0, q1, qh, sg, 2 * hf, w0, w1);
-    iq3s_pair_rt(iq3, q0, q1, qh, sg, 2 * hf + 1, w2, w3);
-    r[0] = (int)w0; r[1] = (int)w1; r[2] = (int)w2; r[3] = (int)w3;
-  }
-  return r;
+// Work-group -> (column tile, row tile). Dense launches are remapped so that each of the 8 XCDs (work-groups are
+// dealt to XCDs round-robin) sweeps a contiguous range of column tiles, row tiles fastest: concurrent work-groups
+// of an XCD share weight tiles in its L2.
+__device__ __forceinline__ void dense_tile(int& nt, int& mtile) {
+  const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
+  int lin = blockIdx.y * gx + blockIdx.x;
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  nt = lin / gy;
+  mtile = lin % gy;
 }
 
 template <int TYPE, int MT, int MODE, bool DUMP>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   constexpr int BM = 32 * MT;
   constexpr bool MINS = Traits<TYPE>::MINS;
+  constexpr bool GU = MODE == GEMM_MOE_GATEUP;
+  constexpr int ACH = BM * 16 / 256;        // 16-byte activation chunks per thread per superblock
+  constexpr int SCH = (8 * BM + 255) / 256;  // scale values per thread per superblock
   __shared__ GemmLds<TYPE, MT> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
   const int K = a.w.K, nb = K / 32, nsb = K / 256;
 
   // ---- which rows: dense (M tile), or one MoE tile (expert e, slots r0 .. r0 + nr - 1)
-  int m0, nvalid, wrow0;
+  int m0, nvalid, wrow0, nt;
   if constexpr (MODE == GEMM_DENSE) {
-    m0 = blockIdx.y * BM;
+    int mtile;
+    dense_tile(nt, mtile);
+    m0 = mtile * BM;
     nvalid = min(BM, a.M - m0);
     wrow0 = 0;
   } else {
@@ -145,103 +177,185 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     m0 = a.tiles[2 + 3 * t];
     nvalid = a.tiles[3 + 3 * t];
     wrow0 = e * a.expert_rows;
+    nt = blockIdx.x;
   }
-  const int n_loc = blockIdx.x * 128 + wave * 32 + lc;  // this lane's weight row (within the expert)
+  const int n_loc = nt * 128 + wave * 32 + lc;  // this lane's weight row (within the expert)
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
   const int n = wrow0 + min(n_loc, n_rows - 1);
 
   if (tid < BM) {
     const int i = min(tid, nvalid - 1);
     int src;
-    if constexpr (MODE == GEMM_DENSE) src = m0 + i;
-    else if constexpr (MODE == GEMM_MOE_GATEUP) src = a.rowmap[m0 + i];
+    if constexpr (MODE == GEMM_MOE_GATEUP) src = a.rowmap[m0 + i];
     else src = m0 + i;
     L.arow[tid] = src;
   }
   if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&L.iq3);
   const KvTab kv = kv_tab();
+  __syncthreads();
 
-  float acc[MT][16], acc2[MODE == GEMM_MOE_GATEUP ? MT : 1][16];
+  // ---- global -> register staging of one superblock's activation rows and scales (issued one superblock ahead)
+  uint4 st_a[ACH];
+  float st_sc[SCH], st_u[SCH];
+#define QM_FETCH_ACTS(SB)                                                                                  \
+  {                                                                                                        \
+    _Pragma("unroll") for (int c = 0; c < ACH; ++c) {                                                      \
+      const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;                                          \
+      st_a[c] = *(const uint4*)(a.aq + (size_t)L.arow[row] * K + (SB) * 256 + col * 16);                   \
+    }                                                                                                      \
+    if constexpr (!DUMP) {                                                                                 \
+      _Pragma("unroll") for (int c = 0; c < SCH; ++c) {                                                    \
+        const int idx = min(tid + 256 * c, 8 * BM - 1), blk = idx / BM, src = L.arow[idx % BM];            \
+        st_sc[c] = a.asc[(size_t)((SB) * 8 + blk) * a.M_stride + src];                                    \
+        if constexpr (MINS) {                                                                              \
+          const int bs = (int)a.absum[(size_t)(2 * ((SB) * 8 + blk)) * a.M_stride + src] +                 \
+                         (int)a.absum[(size_t)(2 * ((SB) * 8 + blk) + 1) * a.M_stride + src];              \
+          st_u[c] = st_sc[c] * (float)bs;                                                                  \
+        }                                                                                                  \
+      }                                                                                                    \
+    }                                                                                                      \
+  }
+#define QM_STORE_ACTS()                                                                                    \
+  {                                                                                                        \
+    _Pragma("unroll") for (int c = 0; c < ACH; ++c) {                                                      \
+      const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;                                          \
+      *(uint4*)(L.a + row * A_STRIDE + col * 16) = st_a[c];                                                \
+    }                                                                                                      \
+    if constexpr (!DUMP) {                                                                                 \
+      _Pragma("unroll") for (int c = 0; c < SCH; ++c) {                                                    \
+        const int idx = tid + 256 * c;                                                                     \
+        if (idx < 8 * BM) {                                                                                \
+          L.asc[idx] = st_sc[c];                                                                           \
+          if constexpr (MINS) L.u[idx] = st_u[c];                                                          \
+        }                                                                                                  \
+      }                                                                                                    \
+    }                                                                                                      \
+  }
+  // ---- this lane's weight row: payloads and header, one superblock ahead (rolling: a block's registers are
+  // reloaded with the next superblock's block as soon as they are consumed)
+  uint4 pay[8], pay2[GU ? 8 : 1];
+  uint4 hdr, hdr2 = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int b = 0; b < 8; ++b) pay[b] = load_payload<TYPE>(a.w, n, b, hf);
+  hdr = load_header<TYPE>(a.w, n, 0);
+  if constexpr (GU) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
-  if constexpr (MODE == GEMM_MOE_GATEUP) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc2[mt][r] = 0.0f;
+    for (int b = 0; b < 8; ++b) pay2[b] = load_payload<TYPE>(a.w2, n, b, hf);
+    hdr2 = load_header<TYPE>(a.w2, n, 0);
   }
 
-  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s = 0; s < nsb; ++s) {
-    __syncthreads();
-    // stage the activation rows of superblock s
+  v16f acc[MT], acc2[GU ? MT : 1];
 #pragma unroll
-    for (int c = tid; c < BM * 16; c += 256) {
-      const int row = c >> 4, col = c & 15;
-      const uint4 v = *(const uint4*)(a.aq + (size_t)L.arow[row] * K + s * 256 + col * 16);
-      *(uint4*)(L.a + row * A_STRIDE + col * 16) = v;
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
+    if constexpr (GU) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc2[mt][r] = 0.0f;
     }
-    for (int c = tid; c < 8 * BM && !DUMP; c += 256) {
-      const int blk = c / BM, i = c % BM, src = L.arow[i];
-      const float sc = a.asc[(size_t)(s * 8 + blk) * a.M_stride + src];
-      L.asc[c] = sc;
-      if constexpr (MINS) {
-        const int bs = (int)a.absum[(size_t)(2 * (s * 8 + blk)) * a.M_stride + src] +
-                       (int)a.absum[(size_t)(2 * (s * 8 + blk) + 1) * a.M_stride + src];
-        L.u[c] = sc * (float)bs;
-      }
-    }
-    __syncthreads();
+  }
+  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v32f zero32;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) zero32[r] = 0.0f;
+
+  QM_FETCH_ACTS(0)
+  QM_STORE_ACTS()
+  __syncthreads();
+
+  for (int s = 0; s < nsb; ++s) {
+    const bool more = s + 1 < nsb;
+    const int sn = more ? s + 1 : s;  // (the last superblock reloads itself: no conditional register state)
+    QM_FETCH_ACTS(sn)
 
     float dsc[8], dmn[8], dsc2[8], dmn2[8];
     int isc[8], isc2[8];
-    sb_scales<TYPE>(a.w, n, s, dsc, dmn, isc);
-    if constexpr (MODE == GEMM_MOE_GATEUP) sb_scales<TYPE>(a.w2, n, s, dsc2, dmn2, isc2);
+    sb_scales<TYPE>(hdr, dsc, dmn, isc);
+    if constexpr (GU) sb_scales<TYPE>(hdr2, dsc2, dmn2, isc2);
+    const uint4 hcur = hdr, hcur2 = hdr2;
+    hdr = load_header<TYPE>(a.w, n, sn);
+    if constexpr (GU) hdr2 = load_header<TYPE>(a.w2, n, sn);
 
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const int blk = s * 8 + b;
-      const v4i bop = b_operand<TYPE>(a.w, (const Iq3Lds*)&L.iq3, kv, n, blk, hf, s);
-      v4i bop2;
-      if constexpr (MODE == GEMM_MOE_GATEUP) bop2 = b_operand<TYPE>(a.w2, (const Iq3Lds*)&L.iq3, kv, n, blk, hf, s);
+    for (int p = 0; p < 4; ++p) {
+      // blocks 2p and 2p+1: lanes of k-half hf carry block 2p+hf's scales into the f32 outer-product MFMAs
+      const float my_dsc = hf ? dsc[2 * p + 1] : dsc[2 * p];
+      const float my_dmn = hf ? -dmn[2 * p + 1] : -dmn[2 * p];
+      const float my_dsc2 = GU ? (hf ? dsc2[2 * p + 1] : dsc2[2 * p]) : 0.0f;
+      v4i bop[2], bop2[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int b = 2 * p + q;
+        bop[q] = b_operand<TYPE>(pay[b], hcur, b, hf, kv, (const Iq3Lds*)&L.iq3);
+        pay[b] = load_payload<TYPE>(a.w, n, sn * 8 + b, hf);
+        if constexpr (GU) {
+          bop2[q] = b_operand<TYPE>(pay2[b], hcur2, b, hf, kv, (const Iq3Lds*)&L.iq3);
+          pay2[b] = load_payload<TYPE>(a.w2, n, sn * 8 + b, hf);
+        }
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint4 av = *(const uint4*)(L.a + (mt * 32 + lc) * A_STRIDE + 32 * b + 16 * hf);
-        const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
-        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, zero16, 0, 0, 0);
-        v16i dv2;
-        if constexpr (MODE == GEMM_MOE_GATEUP) dv2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop2, zero16, 0, 0, 0);
+        v16i dv[2], dv2[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint4 av = *(const uint4*)(L.a + (mt * 32 + lc) * A_STRIDE + 32 * (2 * p + q) + 16 * hf);
+          const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+          dv[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[q], zero16, 0, 0, 0);
+          if constexpr (GU) dv2[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop2[q], zero16, 0, 0, 0);
+        }
         if constexpr (DUMP) {
-          // block sums of rows m0 + i(r), weight row n_loc: isum[(m*rows + n)*nb + blk] = sc * sum
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (i < nvalid && n_loc < n_rows)
-              a.dbg_isum[((size_t)(m0 + i) * n_rows + n_loc) * nb + blk] = isc[b] * dv[r];
-          }
-        } else {
-          float sr[16], ur[16];
+          for (int q = 0; q < 2; ++q)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 v = *(const float4*)(L.asc + b * BM + mt * 32 + 8 * q + 4 * hf);
-            sr[4 * q] = v.x; sr[4 * q + 1] = v.y; sr[4 * q + 2] = v.z; sr[4 * q + 3] = v.w;
-            if constexpr (MINS) {
-              const float4 uv = *(const float4*)(L.u + b * BM + mt * 32 + 8 * q + 4 * hf);
-              ur[4 * q] = uv.x; ur[4 * q + 1] = uv.y; ur[4 * q + 2] = uv.z; ur[4 * q + 3] = uv.w;
+            for (int r = 0; r < 16; ++r) {
+              const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3), blk = s * 8 + 2 * p + q;
+              if (i < nvalid && n_loc < n_rows)
+                a.dbg_isum[((size_t)(m0 + i) * n_rows + n_loc) * nb + blk] = isc[2 * p + q] * dv[q][r];
             }
-          }
+        } else {
+          // s[i][j] = asc[i][b] * dsc[j][b] for both blocks of the pair: one 2-block f32 outer product (lanes
+          // 0-31 carry block 2p, lanes 32-63 block 2p+1; result registers 0-15 / 16-31)
+          const float my_asc = L.asc[(2 * p + hf) * BM + mt * 32 + lc];
+          const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            acc[mt][r] = fmaf(sr[r] * dsc[b], (float)dv[r], acc[mt][r]);
-            if constexpr (MINS) acc[mt][r] = fmaf(ur[r], -dmn[b], acc[mt][r]);
-            if constexpr (MODE == GEMM_MOE_GATEUP) acc2[mt][r] = fmaf(sr[r] * dsc2[b], (float)dv2[r], acc2[mt][r]);
+            acc[mt][r] = fmaf(sc[r], (float)dv[0][r], acc[mt][r]);
+            acc[mt][r] = fmaf(sc[16 + r], (float)dv[1][r], acc[mt][r]);
+          }
+          if constexpr (!MINS) {
+            // (pins the accumulator between block pairs: without it the scheduler overlaps every pair's MFMA
+            //  results and runs out of registers)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
+          }
+          if constexpr (MINS) {
+            // - sum over the pair of (asc * bsum)[i][b] * (dmin * mn)[j][b]: one K=2 f32 MFMA into the accumulator
+            const float my_u = L.u[(2 * p + hf) * BM + mt * 32 + lc];
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(my_u, my_dmn, acc[mt], 0, 0, 0);
+          }
+          if constexpr (GU) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc2[mt][r]));
+            const v32f sc2 = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc2, zero32, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              acc2[mt][r] = fmaf(sc2[r], (float)dv2[0][r], acc2[mt][r]);
+              acc2[mt][r] = fmaf(sc2[16 + r], (float)dv2[1][r], acc2[mt][r]);
+            }
           }
         }
       }
+      // (keeps the scheduler from hoisting every pair's MFMAs together, which needs more than 512 registers)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // every wave is done with superblock s's tile
+    if (more) {
+      QM_STORE_ACTS()
+      __syncthreads();
     }
   }
+#undef QM_FETCH_ACTS
+#undef QM_STORE_ACTS
   if constexpr (DUMP) return;
 
   // ---- epilogue
@@ -302,7 +416,12 @@ template <int TYPE>
 static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
   if (a.dbg_isum) return go<TYPE, 1, GEMM_DENSE, true>(a, s);
   switch (mode) {
-    case GEMM_DENSE: return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
+    case GEMM_DENSE: {
+      // QM_GEMM_MT=1|2 overrides the row tiles per work-group (32 or 64 activation rows)
+      static const int mt_env = getenv("QM_GEMM_MT") ? atoi(getenv("QM_GEMM_MT")) : 0;
+      const int mt = mt_env == 1 || mt_env == 2 ? mt_env : (a.M <= 32 ? 1 : 2);
+      return mt == 1 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
+    }
     case GEMM_MOE_GATEUP: return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN: return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
     default: return hipErrorInvalidValue;
