@@ -37,6 +37,13 @@ struct WView {
 
 __device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)(h & 0xFFFFu))); }
 
+// 16-byte streaming load (non-temporal: weights are read once per product and should not displace cached data)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -46,26 +53,54 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// IQ4_NL codebook as four packed words (bytes kv[4i..4i+3]); values: ggml's kvalues_iq4nl.
-struct KvTab { uint32_t t0, t1, t2, t3; };
-__device__ __forceinline__ KvTab kv_tab() {
+// IQ4_NL / IQ4_XS codebook lookup with two byte permutes and an XOR.
+// v_perm_b32 picks byte `sel` (0..7) of an 8-byte table; for sel 8..11 it returns 0xFF or 0x00 by the sign of table
+// byte 1, 3, 5 or 7, for 12 it returns 0x00 and for 13..15 0xFF. A raw 4-bit code n (0..15) is therefore a valid
+// selector: table A answers codes 0..7 and returns 0x00/0xFF for 8..15, table B (selector n ^ 8) answers codes 8..15
+// and returns 0x00/0xFF for 0..7. Storing each entry pre-XORed with what the other table returns for the same code
+// makes pA ^ pB the codebook value for every code. The junk depends on the tables' own sign bits, so the tables are
+// the fixed point of that rule, computed here at compile time from the codebook.
+struct KvTab { uint32_t a0, a1, b0, b1; };
+namespace detail {
+constexpr uint8_t perm_byte(const uint8_t* in, int sel) {
+  return sel >= 13 ? 0xFF : sel == 12 ? 0x00 : sel >= 8 ? ((in[2 * (sel - 8) + 1] & 0x80) ? 0xFF : 0x00) : in[sel];
+}
+constexpr KvTab make_kv_tab() {
   constexpr int8_t kv[16] = QM_IQ4NL_VALUES_INIT;
-  KvTab t;
-  t.t0 = (uint8_t)kv[0] | ((uint8_t)kv[1] << 8) | ((uint8_t)kv[2] << 16) | ((uint32_t)(uint8_t)kv[3] << 24);
-  t.t1 = (uint8_t)kv[4] | ((uint8_t)kv[5] << 8) | ((uint8_t)kv[6] << 16) | ((uint32_t)(uint8_t)kv[7] << 24);
-  t.t2 = (uint8_t)kv[8] | ((uint8_t)kv[9] << 8) | ((uint8_t)kv[10] << 16) | ((uint32_t)(uint8_t)kv[11] << 24);
-  t.t3 = (uint8_t)kv[12] | ((uint8_t)kv[13] << 8) | ((uint8_t)kv[14] << 16) | ((uint32_t)(uint8_t)kv[15] << 24);
+  uint8_t ta[8] = {}, tb[8] = {};
+  for (int i = 0; i < 8; ++i) {
+    ta[i] = (uint8_t)kv[i];
+    tb[i] = (uint8_t)kv[8 + i];
+  }
+  for (int it = 0; it < 8; ++it) {
+    for (int n = 8; n < 16; ++n) tb[n - 8] = (uint8_t)((uint8_t)kv[n] ^ perm_byte(ta, n));
+    for (int n = 0; n < 8; ++n) ta[n] = (uint8_t)((uint8_t)kv[n] ^ perm_byte(tb, n ^ 8));
+  }
+  KvTab t{};
+  t.a0 = ta[0] | (ta[1] << 8) | (ta[2] << 16) | ((uint32_t)ta[3] << 24);
+  t.a1 = ta[4] | (ta[5] << 8) | (ta[6] << 16) | ((uint32_t)ta[7] << 24);
+  t.b0 = tb[0] | (tb[1] << 8) | (tb[2] << 16) | ((uint32_t)tb[3] << 24);
+  t.b1 = tb[4] | (tb[5] << 8) | (tb[6] << 16) | ((uint32_t)tb[7] << 24);
   return t;
 }
+constexpr bool kv_tab_ok() {
+  constexpr int8_t kv[16] = QM_IQ4NL_VALUES_INIT;
+  const KvTab t = make_kv_tab();
+  const uint8_t ta[8] = {(uint8_t)t.a0, (uint8_t)(t.a0 >> 8), (uint8_t)(t.a0 >> 16), (uint8_t)(t.a0 >> 24),
+                         (uint8_t)t.a1, (uint8_t)(t.a1 >> 8), (uint8_t)(t.a1 >> 16), (uint8_t)(t.a1 >> 24)};
+  const uint8_t tb[8] = {(uint8_t)t.b0, (uint8_t)(t.b0 >> 8), (uint8_t)(t.b0 >> 16), (uint8_t)(t.b0 >> 24),
+                         (uint8_t)t.b1, (uint8_t)(t.b1 >> 8), (uint8_t)(t.b1 >> 16), (uint8_t)(t.b1 >> 24)};
+  for (int n = 0; n < 16; ++n)
+    if ((uint8_t)(perm_byte(ta, n) ^ perm_byte(tb, n ^ 8)) != (uint8_t)kv[n]) return false;
+  return true;
+}
+}  // namespace detail
+static_assert(detail::kv_tab_ok(), "IQ4_NL permute tables do not reproduce the codebook");
+__device__ __forceinline__ KvTab kv_tab() { return detail::make_kv_tab(); }
 
-// Four 4-bit codebook indices (bits 0..3 of each byte of n; bits 4..7 ignored) -> four int8 codebook values.
-// Two byte permutes read the 8-entry halves, a third picks per byte by the index's bit 3.
+// Four 4-bit codes (bits 0..3 of each byte of n, bits 4..7 zero) -> four int8 codebook values.
 __device__ __forceinline__ uint32_t kv_lookup4(const KvTab& t, uint32_t n) {
-  const uint32_t sel = n & 0x07070707u;
-  const uint32_t lo = perm(t.t1, t.t0, sel);
-  const uint32_t hi = perm(t.t3, t.t2, sel);
-  const uint32_t pick = ((n >> 1) & 0x04040404u) | 0x03020100u;
-  return perm(hi, lo, pick);
+  return perm(t.a1, t.a0, n) ^ perm(t.b1, t.b0, n ^ 0x08080808u);
 }
 
 // ---- per-block scale decoding from the header plane

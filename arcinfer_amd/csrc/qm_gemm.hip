@@ -86,8 +86,8 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
       r[0] = (int)(x0 & 0x0F0F0F0Fu); r[1] = (int)(x1 & 0x0F0F0F0Fu);
       r[2] = (int)(x2 & 0x0F0F0F0Fu); r[3] = (int)(x3 & 0x0F0F0F0Fu);
     } else {
-      r[0] = (int)kv_lookup4(kv, x0); r[1] = (int)kv_lookup4(kv, x1);
-      r[2] = (int)kv_lookup4(kv, x2); r[3] = (int)kv_lookup4(kv, x3);
+      r[0] = (int)kv_lookup4(kv, x0 & 0x0F0F0F0Fu); r[1] = (int)kv_lookup4(kv, x1 & 0x0F0F0F0Fu);
+      r[2] = (int)kv_lookup4(kv, x2 & 0x0F0F0F0Fu); r[3] = (int)kv_lookup4(kv, x3 & 0x0F0F0F0Fu);
     }
   } else {
     const uint32_t qh = ((b < 4 ? hdr.x : hdr.y) >> (8 * (b & 3))) & 0xFFu;

@@ -14,61 +14,94 @@ namespace qm {
 template <int TYPE> struct LdsFor { struct type { int unused; }; };
 template <> struct LdsFor<T_IQ3_S> { using type = Iq3Lds; };
 
-// Decodes 32-block b of row n: w[k] = elements 4k..4k+3 (int8x4), integer scale sc (and min mn), float d (dmin).
+// The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0 also q1) and header (h).
+struct RawBlk {
+  uint4 q0, q1, h;
+};
+
+// qrow / hrow: the row's payload and header planes; b: the block
 template <int TYPE>
-__device__ __forceinline__ void decode_block32(const WView& w, const typename LdsFor<TYPE>::type* lds, int n, int b,
+__device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8_t* hrow, int b) {
+  using Tr = Traits<TYPE>;
+  const uint8_t* qp = qrow + (uint32_t)(b * Tr::QB);
+  const uint8_t* hp = hrow + (uint32_t)((b >> 3) * Tr::HB);
+  RawBlk r;
+  r.q1 = make_uint4(0u, 0u, 0u, 0u);
+  r.h = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (TYPE == T_Q8_0) {
+    r.q0 = ld_stream16(qp);
+    r.q1 = ld_stream16(qp + 16);
+    r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (TYPE == T_IQ3_S) {
+    const uint32_t* q = (const uint32_t*)qp;
+    r.q0 = make_uint4(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
+                      __builtin_nontemporal_load(q + 2), 0u);
+    r.h = *(const uint4*)hp;
+  } else {
+    r.q0 = ld_stream16(qp);
+    if constexpr (TYPE == T_IQ4_XS) {
+      const uint2 h = *(const uint2*)hp;
+      r.h.x = h.x;
+      r.h.y = h.y;
+    } else {
+      r.h = *(const uint4*)hp;
+    }
+  }
+  return r;
+}
+
+template <int TYPE>
+__device__ __forceinline__ RawBlk load_block(const WView& w, int n, int b) {
+  using Tr = Traits<TYPE>;
+  return load_block_at<TYPE>(w.qs + (size_t)n * (w.K / 32) * Tr::QB, w.hdr + (size_t)n * (w.K / 256) * Tr::HB, b);
+}
+
+// Decodes a loaded 32-block (index ib = b % 8 in its superblock): w[k] = elements 4k..4k+3 (int8x4), the integer
+// scale sc (and min mn), the float scale d (and dmin).
+template <int TYPE>
+__device__ __forceinline__ void decode_block32(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int ib,
                                                const KvTab& kv, uint32_t wd[8], int& sc, int& mn, float& d,
                                                float& dmin) {
-  using Tr = Traits<TYPE>;
-  const int nb = w.K / 32, nsb = w.K / 256, ib = b & 7;
-  const uint8_t* qp = w.qs + ((size_t)n * nb + b) * Tr::QB;
-  const uint8_t* hp = w.hdr + ((size_t)n * nsb + (b >> 3)) * Tr::HB;
   mn = 0;
   dmin = 0.0f;
   if constexpr (TYPE == T_Q8_0) {
-    const uint4 q0 = *(const uint4*)qp, q1 = *(const uint4*)(qp + 16);
-    wd[0] = q0.x; wd[1] = q0.y; wd[2] = q0.z; wd[3] = q0.w;
-    wd[4] = q1.x; wd[5] = q1.y; wd[6] = q1.z; wd[7] = q1.w;
-    d = h2f(((const uint16_t*)hp)[ib]);
+    wd[0] = r.q0.x; wd[1] = r.q0.y; wd[2] = r.q0.z; wd[3] = r.q0.w;
+    wd[4] = r.q1.x; wd[5] = r.q1.y; wd[6] = r.q1.z; wd[7] = r.q1.w;
+    d = h2f(r.h.x);
     sc = 1;
   } else if constexpr (TYPE == T_Q4_K) {
-    const uint4 q = *(const uint4*)qp;
-    const uint4 h = *(const uint4*)hp;
-    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       wd[k] = qq[k] & 0x0F0F0F0Fu;
       wd[4 + k] = (qq[k] >> 4) & 0x0F0F0F0Fu;
     }
-    d = h2f(h.x);
-    dmin = h2f(h.x >> 16);
-    q4k_scale_min(h.y, h.z, h.w, ib, sc, mn);
+    d = h2f(r.h.x);
+    dmin = h2f(r.h.x >> 16);
+    q4k_scale_min(r.h.y, r.h.z, r.h.w, ib, sc, mn);
   } else if constexpr (TYPE == T_IQ4_XS) {
-    const uint4 q = *(const uint4*)qp;
-    const uint2 h = *(const uint2*)hp;
-    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      wd[k] = kv_lookup4(kv, qq[k]);
-      wd[4 + k] = kv_lookup4(kv, qq[k] >> 4);
+      wd[k] = kv_lookup4(kv, qq[k] & 0x0F0F0F0Fu);
+      wd[4 + k] = kv_lookup4(kv, (qq[k] >> 4) & 0x0F0F0F0Fu);
     }
-    d = h2f(h.x);
-    sc = iq4xs_scale(h.x, h.y, ib);
+    d = h2f(r.h.x);
+    sc = iq4xs_scale(r.h.x, r.h.y, ib);
   } else {  // IQ3_S
-    const uint32_t* qw = (const uint32_t*)qp;
-    const uint32_t q0 = qw[0], q1 = qw[1], sg = qw[2];
-    const uint4 h = *(const uint4*)hp;
-    const uint32_t qh = ((ib < 4 ? h.x : h.y) >> (8 * (ib & 3))) & 0xFFu;
-    iq3s_pair<0>(lds, q0, q1, qh, sg, wd[0], wd[1]);
-    iq3s_pair<1>(lds, q0, q1, qh, sg, wd[2], wd[3]);
-    iq3s_pair<2>(lds, q0, q1, qh, sg, wd[4], wd[5]);
-    iq3s_pair<3>(lds, q0, q1, qh, sg, wd[6], wd[7]);
-    sc = 1 + 2 * (int)((h.z >> (4 * ib)) & 0xFu);
-    d = h2f(h.w);
+    const uint32_t qh = ((ib < 4 ? r.h.x : r.h.y) >> (8 * (ib & 3))) & 0xFFu;
+    iq3s_pair<0>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[0], wd[1]);
+    iq3s_pair<1>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[2], wd[3]);
+    iq3s_pair<2>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[4], wd[5]);
+    iq3s_pair<3>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[6], wd[7]);
+    sc = 1 + 2 * (int)((r.h.z >> (4 * ib)) & 0xFu);
+    d = h2f(r.h.w);
   }
 }
 
-template <int TYPE, int LPR, int R, int TB, bool DUMP>
+// U consecutive iterations of the block loop are loaded before any is decoded, so each lane keeps U*R weight loads
+// in flight (the loop is bandwidth-bound: bytes in flight, not instructions, set its speed).
+template <int TYPE, int LPR, int R, int TB, int U, bool DUMP>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ typename LdsFor<TYPE>::type lds;
   if constexpr (TYPE == T_IQ3_S) {
@@ -88,52 +121,58 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < TB; ++t) acc[r][t] = 0.0f;
 
-  for (int b = gl; b < nb; b += LPR) {
-    uint32_t av[TB][8];
-    float sa[TB];
-    int bs[TB];
+  for (int b0 = gl; b0 < nb; b0 += LPR * U) {
+    RawBlk raw[U][R];
+    uint32_t av[U][TB][8];
+    float sa[U][TB];
+    int bs[U][TB];
 #pragma unroll
-    for (int t = 0; t < TB; ++t) {
-      if (t < T) {
-        const uint4* ap = (const uint4*)(a.aq + (size_t)t * K + 32 * b);
+    for (int u = 0; u < U; ++u) {
+      const int b = min(b0 + LPR * u, nb - 1);  // (past the row's end: reload its last block, masked below)
+#pragma unroll
+      for (int r = 0; r < R; ++r) raw[u][r] = load_block<TYPE>(a.w, min(row0 + r, rows - 1), b);
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        const int tt = min(t, T - 1);
+        const uint4* ap = (const uint4*)(a.aq + (size_t)tt * K + 32 * b);
         const uint4 x0 = ap[0], x1 = ap[1];
-        av[t][0] = x0.x; av[t][1] = x0.y; av[t][2] = x0.z; av[t][3] = x0.w;
-        av[t][4] = x1.x; av[t][5] = x1.y; av[t][6] = x1.z; av[t][7] = x1.w;
-        sa[t] = DUMP ? 0.0f : a.asc[(size_t)b * a.M_stride + t];
+        av[u][t][0] = x0.x; av[u][t][1] = x0.y; av[u][t][2] = x0.z; av[u][t][3] = x0.w;
+        av[u][t][4] = x1.x; av[u][t][5] = x1.y; av[u][t][6] = x1.z; av[u][t][7] = x1.w;
+        sa[u][t] = DUMP ? 0.0f : a.asc[(size_t)b * a.M_stride + tt];
         if constexpr (Traits<TYPE>::MINS)
-          bs[t] = (int)a.absum[(size_t)(2 * b) * a.M_stride + t] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride + t];
+          bs[u][t] = (int)a.absum[(size_t)(2 * b) * a.M_stride + tt] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
         else
-          bs[t] = 0;
-      } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) av[t][k] = 0u;
-        sa[t] = 0.0f;
-        bs[t] = 0;
+          bs[u][t] = 0;
       }
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = min(row0 + r, rows - 1);
-      uint32_t wd[8];
-      int sc, mn;
-      float d, dmin;
-      decode_block32<TYPE>(a.w, &lds, n, b, kv, wd, sc, mn, d, dmin);
+    for (int u = 0; u < U; ++u) {
+      const int b = b0 + LPR * u;
+      const bool live = b < nb;
 #pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        int isum = 0;
+      for (int r = 0; r < R; ++r) {
+        uint32_t wd[8];
+        int sc, mn;
+        float d, dmin;
+        decode_block32<TYPE>(raw[u][r], &lds, b & 7, kv, wd, sc, mn, d, dmin);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) isum = dot4(av[t][k], wd[k], isum);
-        const int iv = sc * isum;
-        if constexpr (DUMP) {
-          if (t < T && row0 + r < rows) {
-            const size_t o = ((size_t)t * rows + (row0 + r)) * nb + b;
-            a.dbg_isum[o] = iv;
-            if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = mn * bs[t];
+        for (int t = 0; t < TB; ++t) {
+          int isum = 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) isum = dot4(av[u][t][k], wd[k], isum);
+          const int iv = sc * isum;
+          if constexpr (DUMP) {
+            if (live && t < T && row0 + r < rows) {
+              const size_t o = ((size_t)t * rows + (row0 + r)) * nb + b;
+              a.dbg_isum[o] = iv;
+              if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = mn * bs[u][t];
+            }
+          } else if (live) {
+            if constexpr (Traits<TYPE>::MINS)
+              acc[r][t] += sa[u][t] * (d * (float)iv - dmin * (float)(mn * bs[u][t]));
+            else
+              acc[r][t] += sa[u][t] * d * (float)iv;
           }
-        } else if constexpr (Traits<TYPE>::MINS) {
-          acc[r][t] += sa[t] * (d * (float)iv - dmin * (float)(mn * bs[t]));
-        } else {
-          acc[r][t] += sa[t] * d * (float)iv;
         }
       }
     }
@@ -153,11 +192,115 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
 }
 
-template <int TYPE, int LPR, int R, int TB, bool DUMP>
+// ---------------------------------------------------------------------------------------------------------------
+// Batch-1 decode GEMV (the token-generation case). The token's int8 row, its per-32 scales (and, for Q4_K, per-32
+// sums) are staged in LDS once per work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each
+// 32-block) so 32 lanes reading consecutive blocks read consecutive 16-byte words. A 32-lane group owns one row at a
+// time: lane j takes blocks j, j + 32, ... of the row, CH of them per step, and the next step's weight loads (next
+// chunk or next row) are issued before the current step is decoded, so every lane keeps 2*CH 16-byte streaming loads
+// in flight. Each group walks `rpg` rows spaced 8 apart (the work-group's 8 groups interleave rows). Requires K/32 to
+// be a multiple of 32.
+template <int TYPE, int CH, bool EXACT>
+__global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
+  extern __shared__ uint4 smem[];
+  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
+  uint8_t* sq = (uint8_t*)smem;            // [2][nb][16] int8 planes
+  float* ssc = (float*)(sq + (size_t)K);    // [nb] scales
+  int* sbs = (int*)(ssc + nb);              // [nb] per-32 sums (Q4_K)
+  const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
+  const int nch = (nb / 32 + CH - 1) / CH;  // steps per row
+  const int row_base = blockIdx.x * 8 * rpg + grp;
+  const int steps = rpg * nch;
+
+  RawBlk cur[CH], nxt[CH];
+  using Tr = Traits<TYPE>;
+  auto fetch = [&](int step, RawBlk* dst) {
+    const int i = step / nch, c = step % nch;
+    const int n = min(row_base + 8 * i, rows - 1);
+    const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
+    const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int b = gl + 32 * (c * CH + u);
+      dst[u] = load_block_at<TYPE>(qrow, hrow, EXACT ? b : min(b, nb - 1));
+    }
+  };
+  fetch(0, cur);
+  // (the first weight loads are in flight while the activations are staged)
+  __shared__ typename LdsFor<TYPE>::type lds;
+  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
+    const int b = i >> 1, h = i & 1;
+    *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
+  }
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    ssc[b] = a.asc[(size_t)b * a.M_stride];
+    if constexpr (Traits<TYPE>::MINS) sbs[b] = (int)a.absum[(size_t)(2 * b) * a.M_stride] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride];
+  }
+  __syncthreads();
+
+  const KvTab kv = kv_tab();
+  float acc = 0.0f;
+  for (int step = 0; step < steps; ++step) {
+    if (step + 1 < steps) fetch(step + 1, nxt);
+    const int i = step / nch, c = step % nch;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int b = gl + 32 * (c * CH + u);
+      if (EXACT || b < nb) {
+        uint32_t wd[8];
+        int sc, mn;
+        float d, dmin;
+        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, mn, d, dmin);
+        const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
+        int isum = dot4(x0.x, wd[0], 0);
+        isum = dot4(x0.y, wd[1], isum);
+        isum = dot4(x0.z, wd[2], isum);
+        isum = dot4(x0.w, wd[3], isum);
+        isum = dot4(x1.x, wd[4], isum);
+        isum = dot4(x1.y, wd[5], isum);
+        isum = dot4(x1.z, wd[6], isum);
+        isum = dot4(x1.w, wd[7], isum);
+        const int iv = __mul24(sc, isum);
+        const float sa = ssc[b];
+        if constexpr (Traits<TYPE>::MINS)
+          acc += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[b]));
+        else
+          acc += sa * d * (float)iv;
+      }
+    }
+    if (c == nch - 1) {
+      const float v = wave_sum_width(acc, 32);
+      const int n = row_base + 8 * i;
+      if (gl == 0 && n < rows) {
+        float* cp = a.C + a.c_off + n;
+        *cp = a.accumulate ? *cp + v : v;
+      }
+      acc = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) cur[u] = nxt[u];
+  }
+}
+
+template <int TYPE, int CH, bool EXACT>
+static hipError_t go1(const GemvArgs& a, hipStream_t s) {
+  const int nb = a.w.K / 32;
+  // rows per 32-lane group: enough work-groups to fill 256 CUs twice, each group walking several rows
+  const int rows = a.w.rows;
+  int rpg = 1;
+  while (rpg < 16 && (rows + 8 * rpg * 2 - 1) / (8 * rpg * 2) >= 1024) rpg *= 2;
+  const unsigned grid = (unsigned)((rows + 8 * rpg - 1) / (8 * rpg));
+  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (Traits<TYPE>::MINS ? sizeof(int) * nb : 0);
+  gemv1_kernel<TYPE, CH, EXACT><<<grid, 256, shm, s>>>(a, rpg);
+  return hipGetLastError();
+}
+
+template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
 static hipError_t go(const GemvArgs& a, hipStream_t s) {
   constexpr int rows_per_wg = 4 * (64 / LPR) * R;
   const dim3 grid((unsigned)((a.w.rows + rows_per_wg - 1) / rows_per_wg)), block(256);
-  gemv_kernel<TYPE, LPR, R, TB, DUMP><<<grid, block, 0, s>>>(a);
+  gemv_kernel<TYPE, LPR, R, TB, U, DUMP><<<grid, block, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -173,6 +316,12 @@ static hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
     }
   }
   const bool l32 = nb % 32 == 0;
+  if (a.T <= 1 && l32 && a.w.K <= 32768 && TYPE != T_IQ3_S) {
+    const int per_lane = nb / 32;  // blocks per lane per row
+    if (per_lane % 5 == 0) return go1<TYPE, 5, true>(a, s);
+    if (per_lane % 4 == 0) return go1<TYPE, 4, true>(a, s);
+    return go1<TYPE, 6, false>(a, s);
+  }
   if (a.T <= 1) {
     // short rows (many rows): 2 rows per lane group; long rows (few rows, K >= 8192): 1, for more waves in flight
     if (l32) return a.w.K >= 8192 ? go<TYPE, 32, 1, 1, false>(a, s) : go<TYPE, 32, 2, 1, false>(a, s);
