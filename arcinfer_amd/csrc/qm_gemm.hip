@@ -27,9 +27,10 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 constexpr int A_STRIDE = 272;  // LDS bytes per staged activation row
 
 template <int TYPE, int MT> struct GemmLds {
-  alignas(16) uint8_t a[32 * MT * A_STRIDE];
-  alignas(16) float asc[8 * 32 * MT];
-  float u[Traits<TYPE>::MINS ? 8 * 32 * MT : 1];
+  // (two buffers: superblock s is read from one while superblock s + 1 is written into the other)
+  alignas(16) uint8_t a[2][32 * MT * A_STRIDE];
+  alignas(16) float asc[2][8 * 32 * MT];
+  float u[2][Traits<TYPE>::MINS ? 8 * 32 * MT : 1];
   int arow[32 * MT];
   typename std::conditional<TYPE == T_IQ3_S, Iq3Lds, int>::type iq3;
 };
@@ -151,6 +152,11 @@ __device__ __forceinline__ void dense_tile(int& nt, int& mtile) {
   mtile = lin % gy;
 }
 
+// lo in lanes where m is 0, hi where m is all ones
+__device__ __forceinline__ float lane_pick(uint32_t m, float lo, float hi) {
+  return __uint_as_float((__float_as_uint(lo) & ~m) | (__float_as_uint(hi) & m));
+}
+
 template <int TYPE, int MT, int MODE, bool DUMP>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   constexpr int BM = 32 * MT;
@@ -192,16 +198,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   }
   if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&L.iq3);
   const KvTab kv = kv_tab();
+  const uint32_t hfm = 0u - (uint32_t)hf;  // all ones in the upper half-wave
   __syncthreads();
 
   // ---- global -> register staging of one superblock's activation rows and scales (issued one superblock ahead)
-  uint4 st_a[ACH];
+  u32x4_t st_a[ACH];  // (a native vector type: an array of HIP's uint4 structs is kept in scratch memory)
   float st_sc[SCH], st_u[SCH];
 #define QM_FETCH_ACTS(SB)                                                                                  \
   {                                                                                                        \
     _Pragma("unroll") for (int c = 0; c < ACH; ++c) {                                                      \
       const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;                                          \
-      st_a[c] = *(const uint4*)(a.aq + (size_t)L.arow[row] * K + (SB) * 256 + col * 16);                   \
+      st_a[c] = *(const u32x4_t*)(a.aq + (size_t)L.arow[row] * K + (SB) * 256 + col * 16);                   \
     }                                                                                                      \
     if constexpr (!DUMP) {                                                                                 \
       _Pragma("unroll") for (int c = 0; c < SCH; ++c) {                                                    \
@@ -215,18 +222,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       }                                                                                                    \
     }                                                                                                      \
   }
-#define QM_STORE_ACTS()                                                                                    \
+#define QM_STORE_ACTS(BUF)                                                                                 \
   {                                                                                                        \
     _Pragma("unroll") for (int c = 0; c < ACH; ++c) {                                                      \
       const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;                                          \
-      *(uint4*)(L.a + row * A_STRIDE + col * 16) = st_a[c];                                                \
+      *(u32x4_t*)(L.a[BUF] + row * A_STRIDE + col * 16) = st_a[c];                                        \
     }                                                                                                      \
     if constexpr (!DUMP) {                                                                                 \
       _Pragma("unroll") for (int c = 0; c < SCH; ++c) {                                                    \
         const int idx = tid + 256 * c;                                                                     \
         if (idx < 8 * BM) {                                                                                \
-          L.asc[idx] = st_sc[c];                                                                           \
-          if constexpr (MINS) L.u[idx] = st_u[c];                                                          \
+          L.asc[BUF][idx] = st_sc[c];                                                                      \
+          if constexpr (MINS) L.u[BUF][idx] = st_u[c];                                                     \
         }                                                                                                  \
       }                                                                                                    \
     }                                                                                                      \
@@ -260,12 +267,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   for (int r = 0; r < 32; ++r) zero32[r] = 0.0f;
 
   QM_FETCH_ACTS(0)
-  QM_STORE_ACTS()
+  QM_STORE_ACTS(0)
   __syncthreads();
 
   for (int s = 0; s < nsb; ++s) {
-    const bool more = s + 1 < nsb;
-    const int sn = more ? s + 1 : s;  // (the last superblock reloads itself: no conditional register state)
+    const int cur = s & 1;
+    const int sn = s + 1 < nsb ? s + 1 : s;  // (the last superblock reloads itself: no conditional register state)
     QM_FETCH_ACTS(sn)
 
     float dsc[8], dmn[8], dsc2[8], dmn2[8];
@@ -278,10 +285,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
+      // superblock sn's activations into the other buffer, halfway through (its loads have had two pairs' time;
+      // that buffer's last readers passed the barrier that ended the previous superblock)
+      if (p == 2) QM_STORE_ACTS(cur ^ 1)
       // blocks 2p and 2p+1: lanes of k-half hf carry block 2p+hf's scales into the f32 outer-product MFMAs
-      const float my_dsc = hf ? dsc[2 * p + 1] : dsc[2 * p];
-      const float my_dmn = hf ? -dmn[2 * p + 1] : -dmn[2 * p];
-      const float my_dsc2 = GU ? (hf ? dsc2[2 * p + 1] : dsc2[2 * p]) : 0.0f;
+      // (a bit select, not hf ? x[2p+1] : x[2p]: the compiler turns that into a lane-dependent index into the
+      //  array, which it then keeps in scratch memory)
+      const float my_dsc = lane_pick(hfm, dsc[2 * p], dsc[2 * p + 1]);
+      const float my_dmn = -lane_pick(hfm, dmn[2 * p], dmn[2 * p + 1]);
+      const float my_dsc2 = GU ? lane_pick(hfm, dsc2[2 * p], dsc2[2 * p + 1]) : 0.0f;
       v4i bop[2], bop2[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -298,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         v16i dv[2], dv2[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          const uint4 av = *(const uint4*)(L.a + (mt * 32 + lc) * A_STRIDE + 32 * (2 * p + q) + 16 * hf);
+          const uint4 av = *(const uint4*)(L.a[cur] + (mt * 32 + lc) * A_STRIDE + 32 * (2 * p + q) + 16 * hf);
           const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
           dv[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[q], zero16, 0, 0, 0);
           if constexpr (GU) dv2[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop2[q], zero16, 0, 0, 0);
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         } else {
           // s[i][j] = asc[i][b] * dsc[j][b] for both blocks of the pair: one 2-block f32 outer product (lanes
           // 0-31 carry block 2p, lanes 32-63 block 2p+1; result registers 0-15 / 16-31)
-          const float my_asc = L.asc[(2 * p + hf) * BM + mt * 32 + lc];
+          const float my_asc = L.asc[cur][(2 * p + hf) * BM + mt * 32 + lc];
           const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -330,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
           }
           if constexpr (MINS) {
             // - sum over the pair of (asc * bsum)[i][b] * (dmin * mn)[j][b]: one K=2 f32 MFMA into the accumulator
-            const float my_u = L.u[(2 * p + hf) * BM + mt * 32 + lc];
+            const float my_u = L.u[cur][(2 * p + hf) * BM + mt * 32 + lc];
             acc[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(my_u, my_dmn, acc[mt], 0, 0, 0);
           }
           if constexpr (GU) {
@@ -348,11 +360,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       // (keeps the scheduler from hoisting every pair's MFMAs together, which needs more than 512 registers)
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // every wave is done with superblock s's tile
-    if (more) {
-      QM_STORE_ACTS()
-      __syncthreads();
-    }
+    __syncthreads();  // superblock s's buffer is free, superblock sn's is complete
   }
 #undef QM_FETCH_ACTS
 #undef QM_STORE_ACTS
