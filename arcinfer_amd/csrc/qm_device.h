@@ -39,9 +39,8 @@ __device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_
 
 // 16-byte streaming load (non-temporal: weights are read once per product and should not displace cached data)
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_stream16(const void* p) {
-  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
-  return make_uint4(v[0], v[1], v[2], v[3]);
+__device__ __forceinline__ u32x4_t ld_stream16(const void* p) {
+  return __builtin_nontemporal_load((const u32x4_t*)p);
 }
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

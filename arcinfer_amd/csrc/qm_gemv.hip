@@ -15,8 +15,9 @@ template <int TYPE> struct LdsFor { struct type { int unused; }; };
 template <> struct LdsFor<T_IQ3_S> { using type = Iq3Lds; };
 
 // The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0 also q1) and header (h).
+// (native vector members: arrays of structs holding HIP's uint4 are kept in scratch memory)
 struct RawBlk {
-  uint4 q0, q1, h;
+  u32x4_t q0, q1, h;
 };
 
 // qrow / hrow: the row's payload and header planes; b: the block
@@ -26,17 +27,17 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
   const uint8_t* qp = qrow + (uint32_t)(b * Tr::QB);
   const uint8_t* hp = hrow + (uint32_t)((b >> 3) * Tr::HB);
   RawBlk r;
-  r.q1 = make_uint4(0u, 0u, 0u, 0u);
-  r.h = make_uint4(0u, 0u, 0u, 0u);
+  r.q1 = u32x4_t{0u, 0u, 0u, 0u};
+  r.h = u32x4_t{0u, 0u, 0u, 0u};
   if constexpr (TYPE == T_Q8_0) {
     r.q0 = ld_stream16(qp);
     r.q1 = ld_stream16(qp + 16);
     r.h.x = ((const uint16_t*)hp)[b & 7];
   } else if constexpr (TYPE == T_IQ3_S) {
     const uint32_t* q = (const uint32_t*)qp;
-    r.q0 = make_uint4(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
-                      __builtin_nontemporal_load(q + 2), 0u);
-    r.h = *(const uint4*)hp;
+    r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2),
+                   0u};
+    r.h = *(const u32x4_t*)hp;
   } else {
     r.q0 = ld_stream16(qp);
     if constexpr (TYPE == T_IQ4_XS) {
@@ -44,7 +45,7 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
       r.h.x = h.x;
       r.h.y = h.y;
     } else {
-      r.h = *(const uint4*)hp;
+      r.h = *(const u32x4_t*)hp;
     }
   }
   return r;
@@ -316,7 +317,7 @@ static hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
     }
   }
   const bool l32 = nb % 32 == 0;
-  if (a.T <= 1 && l32 && a.w.K <= 32768 && TYPE != T_IQ3_S) {
+  if (a.T <= 1 && l32 && a.w.K <= 32768) {
     const int per_lane = nb / 32;  // blocks per lane per row
     if (per_lane % 5 == 0) return go1<TYPE, 5, true>(a, s);
     if (per_lane % 4 == 0) return go1<TYPE, 4, true>(a, s);
