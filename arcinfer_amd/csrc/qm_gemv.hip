@@ -7,6 +7,8 @@
 // masks from LDS), takes 8 v_dot4_i32_i8 per token and scales the int32 block sum in f32 -- per block exactly
 // the reference's expression `sa * d * (float)(sc0 * lo + sc1 * hi)` (zero/kernels/decode.cl:695-706, 1107-1115),
 // with the min term for Q4_K. A cross-lane butterfly then sums the group's partial results.
+#include <stdlib.h>
+
 #include "qm_launch.h"
 
 namespace qm {
@@ -284,6 +286,112 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Batch-1 decode GEMV, persistent sweep. LPR lanes share a row (32, or 128 = two waves with an LDS combine); lane j
+// takes blocks j, j + LPR, ... (CH of them). The grid is a few work-groups per CU and lane group g walks rows
+// g, g + G, g + 2G, ... (G = lane groups in the grid), so the whole grid moves through the weight matrix together
+// and every group has one row in flight: it decodes the row once its loads land and only then issues the next row's
+// loads. Measured on MI355X this beats both issuing every row's loads up front (the decode then piles up behind the
+// stream) and keeping two rows in flight per group. The token's activations are staged in LDS once per work-group, as in gemv1_kernel.
+template <int TYPE, int LPR, int CH, bool EXACT>
+__global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
+  extern __shared__ uint4 smem[];
+  using Tr = Traits<TYPE>;
+  constexpr int GPW = 256 / LPR;                 // lane groups per work-group
+  constexpr int WPR = LPR > 64 ? LPR / 64 : 1;   // waves per row
+  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
+  uint8_t* sq = (uint8_t*)smem;              // [2][nb][16] int8 planes
+  float* ssc = (float*)(sq + (size_t)K);      // [nb]
+  int* sbs = (int*)(ssc + nb);                // [nb] (Q4_K)
+  __shared__ typename LdsFor<TYPE>::type lds;
+  __shared__ float part[2][GPW][WPR];
+  const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+  const int G = gridDim.x * GPW;
+  const int g0 = blockIdx.x * GPW + grp;
+  // steps: the group's rows; with two waves per row every group of the work-group runs the same number of steps
+  // (the combine's barrier), the extra steps of the shorter groups recomputing the last row without storing it
+  const int steps = WPR == 1 ? (g0 < rows ? (rows - 1 - g0) / G + 1 : 0) : (rows - 1 - (int)blockIdx.x * GPW) / G + 1;
+  RawBlk cur[CH];
+  auto fetch = [&](int i, RawBlk* dst) {
+    const int n = min(g0 + G * i, rows - 1);
+    const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
+    const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int b = gl + LPR * u;
+      dst[u] = load_block_at<TYPE>(qrow, hrow, EXACT ? b : min(b, nb - 1));
+    }
+  };
+  fetch(0, cur);
+  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
+    const int b = i >> 1, h = i & 1;
+    *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
+  }
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    ssc[b] = a.asc[(size_t)b * a.M_stride];
+    if constexpr (Tr::MINS) sbs[b] = (int)a.absum[(size_t)(2 * b) * a.M_stride] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride];
+  }
+  __syncthreads();
+  const KvTab kv = kv_tab();
+  for (int i = 0; i < steps; ++i) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int b = gl + LPR * u;
+      if (EXACT || b < nb) {
+        uint32_t wd[8];
+        int sc, mn;
+        float d, dmin;
+        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, mn, d, dmin);
+        const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
+        int isum = dot4(x0.x, wd[0], 0);
+        isum = dot4(x0.y, wd[1], isum);
+        isum = dot4(x0.z, wd[2], isum);
+        isum = dot4(x0.w, wd[3], isum);
+        isum = dot4(x1.x, wd[4], isum);
+        isum = dot4(x1.y, wd[5], isum);
+        isum = dot4(x1.z, wd[6], isum);
+        isum = dot4(x1.w, wd[7], isum);
+        const int iv = __mul24(sc, isum);
+        const float sa = ssc[b];
+        if constexpr (Tr::MINS)
+          acc += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[b]));
+        else
+          acc += sa * d * (float)iv;
+      }
+    }
+    fetch(i + 1, cur);  // (unconditional and clamped to the last row: no branch between the decode and the loads)
+    const int n = g0 + G * i;
+    float v;
+    if constexpr (WPR == 1) {
+      v = wave_sum_width(acc, LPR);
+    } else {
+      const float w = wave_sum_width(acc, 64);
+      if ((threadIdx.x & 63) == 0) part[i & 1][grp][gl >> 6] = w;
+      __syncthreads();  // (double-buffered by step parity: one barrier per step)
+      v = part[i & 1][grp][0];
+#pragma unroll
+      for (int k = 1; k < WPR; ++k) v += part[i & 1][grp][k];
+    }
+    if (gl == 0 && n < rows) {
+      float* cp = a.C + a.c_off + n;
+      *cp = a.accumulate ? *cp + v : v;
+    }
+  }
+}
+
+template <int TYPE, int LPR, int CH, bool EXACT>
+static hipError_t gos(const GemvArgs& a, hipStream_t s) {
+  constexpr int GPW = 256 / LPR;
+  const int nb = a.w.K / 32;
+  // two work-groups per CU (256 CUs), fewer when the matrix has fewer rows than lane groups
+  const int wgs = min(512, (a.w.rows + GPW - 1) / GPW);
+  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (Traits<TYPE>::MINS ? sizeof(int) * nb : 0);
+  gemvs_kernel<TYPE, LPR, CH, EXACT><<<wgs, 256, shm, s>>>(a);
+  return hipGetLastError();
+}
+
 template <int TYPE, int CH, bool EXACT>
 static hipError_t go1(const GemvArgs& a, hipStream_t s) {
   const int nb = a.w.K / 32;
@@ -317,6 +425,30 @@ static hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
     }
   }
   const bool l32 = nb % 32 == 0;
+  static const int sweep = getenv("QM_GEMV_SWEEP") ? atoi(getenv("QM_GEMV_SWEEP")) : 1;
+  if (a.T <= 1 && sweep && a.w.K <= 32768) {
+    if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
+      switch ((nb + 31) / 32) {
+        case 1: return nb == 32 ? gos<TYPE, 32, 1, true>(a, s) : gos<TYPE, 32, 1, false>(a, s);
+        case 2: return nb == 64 ? gos<TYPE, 32, 2, true>(a, s) : gos<TYPE, 32, 2, false>(a, s);
+        case 3: return nb == 96 ? gos<TYPE, 32, 3, true>(a, s) : gos<TYPE, 32, 3, false>(a, s);
+        case 4: return nb == 128 ? gos<TYPE, 32, 4, true>(a, s) : gos<TYPE, 32, 4, false>(a, s);
+        case 5: return nb == 160 ? gos<TYPE, 32, 5, true>(a, s) : gos<TYPE, 32, 5, false>(a, s);
+        case 6: return nb == 192 ? gos<TYPE, 32, 6, true>(a, s) : gos<TYPE, 32, 6, false>(a, s);
+        case 7: return nb == 224 ? gos<TYPE, 32, 7, true>(a, s) : gos<TYPE, 32, 7, false>(a, s);
+        default: return nb == 256 ? gos<TYPE, 32, 8, true>(a, s) : gos<TYPE, 32, 8, false>(a, s);
+      }
+    }
+    // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
+    switch ((nb + 127) / 128) {
+      case 3: return nb == 384 ? gos<TYPE, 128, 3, true>(a, s) : gos<TYPE, 128, 3, false>(a, s);
+      case 4: return nb == 512 ? gos<TYPE, 128, 4, true>(a, s) : gos<TYPE, 128, 4, false>(a, s);
+      case 5: return nb == 640 ? gos<TYPE, 128, 5, true>(a, s) : gos<TYPE, 128, 5, false>(a, s);
+      case 6: return nb == 768 ? gos<TYPE, 128, 6, true>(a, s) : gos<TYPE, 128, 6, false>(a, s);
+      case 7: return nb == 896 ? gos<TYPE, 128, 7, true>(a, s) : gos<TYPE, 128, 7, false>(a, s);
+      default: return nb == 1024 ? gos<TYPE, 128, 8, true>(a, s) : gos<TYPE, 128, 8, false>(a, s);
+    }
+  }
   if (a.T <= 1 && l32 && a.w.K <= 32768) {
     const int per_lane = nb / 32;  // blocks per lane per row
     if (per_lane % 5 == 0) return go1<TYPE, 5, true>(a, s);
