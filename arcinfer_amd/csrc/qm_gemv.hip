@@ -293,18 +293,19 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
 // and every group has one row in flight: it decodes the row once its loads land and only then issues the next row's
 // loads. Measured on MI355X this beats both issuing every row's loads up front (the decode then piles up behind the
 // stream) and keeping two rows in flight per group. The token's activations are staged in LDS once per work-group, as in gemv1_kernel.
-template <int TYPE, int LPR, int CH, bool EXACT>
+template <int TYPE, int LPR, int CH, bool EXACT, int TB>
 __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   extern __shared__ uint4 smem[];
   using Tr = Traits<TYPE>;
   constexpr int GPW = 256 / LPR;                 // lane groups per work-group
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;   // waves per row
-  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
-  uint8_t* sq = (uint8_t*)smem;              // [2][nb][16] int8 planes
-  float* ssc = (float*)(sq + (size_t)K);      // [nb]
-  int* sbs = (int*)(ssc + nb);                // [nb] (Q4_K)
+  const int K = a.w.K, nb = K / 32, rows = a.w.rows, T = a.T;
+  // LDS: per token t < TB: int8 planes [2][nb][16] at t*K, then scales [TB][nb], then Q4_K block sums [TB][nb]
+  uint8_t* sq = (uint8_t*)smem;
+  float* ssc = (float*)(sq + (size_t)TB * K);
+  int* sbs = (int*)(ssc + (size_t)TB * nb);
   __shared__ typename LdsFor<TYPE>::type lds;
-  __shared__ float part[2][GPW][WPR];
+  __shared__ float part[2][GPW][WPR][TB];
   const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
   const int G = gridDim.x * GPW;
   const int g0 = blockIdx.x * GPW + grp;
@@ -324,18 +325,23 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   };
   fetch(0, cur);
   if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
-  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
-    const int b = i >> 1, h = i & 1;
-    *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
+  for (int i = threadIdx.x; i < 2 * nb * TB; i += 256) {
+    const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
+    const int tt = min(t, T - 1);  // (tokens past T: a copy of the last, never stored)
+    *(uint4*)(sq + (size_t)t * K + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + (size_t)tt * K + 32 * b + 16 * h);
   }
-  for (int b = threadIdx.x; b < nb; b += 256) {
-    ssc[b] = a.asc[(size_t)b * a.M_stride];
-    if constexpr (Tr::MINS) sbs[b] = (int)a.absum[(size_t)(2 * b) * a.M_stride] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride];
+  for (int i = threadIdx.x; i < nb * TB; i += 256) {
+    const int t = i / nb, b = i % nb, tt = min(t, T - 1);
+    ssc[i] = a.asc[(size_t)b * a.M_stride + tt];
+    if constexpr (Tr::MINS)
+      sbs[i] = (int)a.absum[(size_t)(2 * b) * a.M_stride + tt] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
   }
   __syncthreads();
   const KvTab kv = kv_tab();
   for (int i = 0; i < steps; ++i) {
-    float acc = 0.0f;
+    float acc[TB];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) acc[t] = 0.0f;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int b = gl + LPR * u;
@@ -344,52 +350,81 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
         int sc, mn;
         float d, dmin;
         decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, mn, d, dmin);
-        const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
-        int isum = dot4(x0.x, wd[0], 0);
-        isum = dot4(x0.y, wd[1], isum);
-        isum = dot4(x0.z, wd[2], isum);
-        isum = dot4(x0.w, wd[3], isum);
-        isum = dot4(x1.x, wd[4], isum);
-        isum = dot4(x1.y, wd[5], isum);
-        isum = dot4(x1.z, wd[6], isum);
-        isum = dot4(x1.w, wd[7], isum);
-        const int iv = __mul24(sc, isum);
-        const float sa = ssc[b];
-        if constexpr (Tr::MINS)
-          acc += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[b]));
-        else
-          acc += sa * d * (float)iv;
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          const uint8_t* st = sq + (size_t)t * K;
+          const uint4 x0 = *(const uint4*)(st + b * 16), x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
+          int isum = dot4(x0.x, wd[0], 0);
+          isum = dot4(x0.y, wd[1], isum);
+          isum = dot4(x0.z, wd[2], isum);
+          isum = dot4(x0.w, wd[3], isum);
+          isum = dot4(x1.x, wd[4], isum);
+          isum = dot4(x1.y, wd[5], isum);
+          isum = dot4(x1.z, wd[6], isum);
+          isum = dot4(x1.w, wd[7], isum);
+          const int iv = __mul24(sc, isum);
+          const float sa = ssc[t * nb + b];
+          if constexpr (Tr::MINS)
+            acc[t] += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[t * nb + b]));
+          else
+            acc[t] += sa * d * (float)iv;
+        }
       }
     }
     fetch(i + 1, cur);  // (unconditional and clamped to the last row: no branch between the decode and the loads)
     const int n = g0 + G * i;
-    float v;
+    float v[TB];
     if constexpr (WPR == 1) {
-      v = wave_sum_width(acc, LPR);
-    } else {
-      const float w = wave_sum_width(acc, 64);
-      if ((threadIdx.x & 63) == 0) part[i & 1][grp][gl >> 6] = w;
-      __syncthreads();  // (double-buffered by step parity: one barrier per step)
-      v = part[i & 1][grp][0];
 #pragma unroll
-      for (int k = 1; k < WPR; ++k) v += part[i & 1][grp][k];
+      for (int t = 0; t < TB; ++t) v[t] = wave_sum_width(acc[t], LPR);
+    } else {
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        const float w = wave_sum_width(acc[t], 64);
+        if ((threadIdx.x & 63) == 0) part[i & 1][grp][gl >> 6][t] = w;
+      }
+      __syncthreads();  // (double-buffered by step parity: one barrier per step)
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        v[t] = part[i & 1][grp][0][t];
+#pragma unroll
+        for (int k = 1; k < WPR; ++k) v[t] += part[i & 1][grp][k][t];
+      }
     }
     if (gl == 0 && n < rows) {
-      float* cp = a.C + a.c_off + n;
-      *cp = a.accumulate ? *cp + v : v;
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+        if (t < T) {
+          float* cp = a.C + (size_t)t * a.ldc + a.c_off + n;
+          *cp = a.accumulate ? *cp + v[t] : v[t];
+        }
     }
   }
 }
 
-template <int TYPE, int LPR, int CH, bool EXACT>
+// LDS bytes of gemvs_kernel for TB tokens
+static size_t gemvs_lds(int type, int K, int TB) {
+  const int nb = K / 32;
+  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K ? sizeof(int) * nb : 0));
+}
+
+template <int TYPE, int LPR, int CH, bool EXACT, int TB>
 static hipError_t gos(const GemvArgs& a, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
-  const int nb = a.w.K / 32;
   // two work-groups per CU (256 CUs), fewer when the matrix has fewer rows than lane groups
   const int wgs = min(512, (a.w.rows + GPW - 1) / GPW);
-  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (Traits<TYPE>::MINS ? sizeof(int) * nb : 0);
-  gemvs_kernel<TYPE, LPR, CH, EXACT><<<wgs, 256, shm, s>>>(a);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
+}
+
+template <int TYPE, int LPR, int CH, bool EXACT>
+static hipError_t gos_tb(const GemvArgs& a, hipStream_t s) {
+  switch (a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8) {
+    case 1: return gos<TYPE, LPR, CH, EXACT, 1>(a, s);
+    case 2: return gos<TYPE, LPR, CH, EXACT, 2>(a, s);
+    case 4: return gos<TYPE, LPR, CH, EXACT, 4>(a, s);
+    default: return gos<TYPE, LPR, CH, EXACT, 8>(a, s);
+  }
 }
 
 template <int TYPE, int CH, bool EXACT>
@@ -426,27 +461,44 @@ static hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
   }
   const bool l32 = nb % 32 == 0;
   static const int sweep = getenv("QM_GEMV_SWEEP") ? atoi(getenv("QM_GEMV_SWEEP")) : 1;
-  if (a.T <= 1 && sweep && a.w.K <= 32768) {
-    if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
-      switch ((nb + 31) / 32) {
-        case 1: return nb == 32 ? gos<TYPE, 32, 1, true>(a, s) : gos<TYPE, 32, 1, false>(a, s);
-        case 2: return nb == 64 ? gos<TYPE, 32, 2, true>(a, s) : gos<TYPE, 32, 2, false>(a, s);
-        case 3: return nb == 96 ? gos<TYPE, 32, 3, true>(a, s) : gos<TYPE, 32, 3, false>(a, s);
-        case 4: return nb == 128 ? gos<TYPE, 32, 4, true>(a, s) : gos<TYPE, 32, 4, false>(a, s);
-        case 5: return nb == 160 ? gos<TYPE, 32, 5, true>(a, s) : gos<TYPE, 32, 5, false>(a, s);
-        case 6: return nb == 192 ? gos<TYPE, 32, 6, true>(a, s) : gos<TYPE, 32, 6, false>(a, s);
-        case 7: return nb == 224 ? gos<TYPE, 32, 7, true>(a, s) : gos<TYPE, 32, 7, false>(a, s);
-        default: return nb == 256 ? gos<TYPE, 32, 8, true>(a, s) : gos<TYPE, 32, 8, false>(a, s);
+  if (sweep && nb <= 1024) {
+    // tokens per launch: as many as fit in 80 KB of LDS (two work-groups per CU), up to 8; more tokens -> chunks
+    // of tokens, each launch reading the weights once
+    int tb = 8;
+    while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > 80 * 1024) tb >>= 1;
+    if (gemvs_lds(TYPE, a.w.K, tb) <= 80 * 1024) {
+      for (int t0 = 0; t0 < a.T; t0 += tb) {
+        GemvArgs c = a;
+        c.T = min(tb, a.T - t0);
+        c.aq = a.aq + (size_t)t0 * a.w.K;
+        c.asc = a.asc + t0;
+        c.absum = a.absum + t0;
+        c.C = a.C + (size_t)t0 * a.ldc;
+        hipError_t e;
+        if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
+          switch ((nb + 31) / 32) {
+            case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true>(c, s) : gos_tb<TYPE, 32, 1, false>(c, s); break;
+            case 2: e = nb == 64 ? gos_tb<TYPE, 32, 2, true>(c, s) : gos_tb<TYPE, 32, 2, false>(c, s); break;
+            case 3: e = nb == 96 ? gos_tb<TYPE, 32, 3, true>(c, s) : gos_tb<TYPE, 32, 3, false>(c, s); break;
+            case 4: e = nb == 128 ? gos_tb<TYPE, 32, 4, true>(c, s) : gos_tb<TYPE, 32, 4, false>(c, s); break;
+            case 5: e = nb == 160 ? gos_tb<TYPE, 32, 5, true>(c, s) : gos_tb<TYPE, 32, 5, false>(c, s); break;
+            case 6: e = nb == 192 ? gos_tb<TYPE, 32, 6, true>(c, s) : gos_tb<TYPE, 32, 6, false>(c, s); break;
+            case 7: e = nb == 224 ? gos_tb<TYPE, 32, 7, true>(c, s) : gos_tb<TYPE, 32, 7, false>(c, s); break;
+            default: e = nb == 256 ? gos_tb<TYPE, 32, 8, true>(c, s) : gos_tb<TYPE, 32, 8, false>(c, s); break;
+          }
+        } else {  // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
+          switch ((nb + 127) / 128) {
+            case 3: e = nb == 384 ? gos_tb<TYPE, 128, 3, true>(c, s) : gos_tb<TYPE, 128, 3, false>(c, s); break;
+            case 4: e = nb == 512 ? gos_tb<TYPE, 128, 4, true>(c, s) : gos_tb<TYPE, 128, 4, false>(c, s); break;
+            case 5: e = nb == 640 ? gos_tb<TYPE, 128, 5, true>(c, s) : gos_tb<TYPE, 128, 5, false>(c, s); break;
+            case 6: e = nb == 768 ? gos_tb<TYPE, 128, 6, true>(c, s) : gos_tb<TYPE, 128, 6, false>(c, s); break;
+            case 7: e = nb == 896 ? gos_tb<TYPE, 128, 7, true>(c, s) : gos_tb<TYPE, 128, 7, false>(c, s); break;
+            default: e = nb == 1024 ? gos_tb<TYPE, 128, 8, true>(c, s) : gos_tb<TYPE, 128, 8, false>(c, s); break;
+          }
+        }
+        if (e != hipSuccess) return e;
       }
-    }
-    // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
-    switch ((nb + 127) / 128) {
-      case 3: return nb == 384 ? gos<TYPE, 128, 3, true>(a, s) : gos<TYPE, 128, 3, false>(a, s);
-      case 4: return nb == 512 ? gos<TYPE, 128, 4, true>(a, s) : gos<TYPE, 128, 4, false>(a, s);
-      case 5: return nb == 640 ? gos<TYPE, 128, 5, true>(a, s) : gos<TYPE, 128, 5, false>(a, s);
-      case 6: return nb == 768 ? gos<TYPE, 128, 6, true>(a, s) : gos<TYPE, 128, 6, false>(a, s);
-      case 7: return nb == 896 ? gos<TYPE, 128, 7, true>(a, s) : gos<TYPE, 128, 7, false>(a, s);
-      default: return nb == 1024 ? gos<TYPE, 128, 8, true>(a, s) : gos<TYPE, 128, 8, false>(a, s);
+      return hipSuccess;
     }
   }
   if (a.T <= 1 && l32 && a.w.K <= 32768) {

@@ -147,6 +147,20 @@ def main():
             per[f"{K}->{N}"] = {"us_per_launch": round(ms1 * 1e3, 2), "GB/s": round(b / (ms1 * 1e-3) / 1e9, 1),
                                "weight_bytes": b}
         out["gemv_per_matrix"] = per
+        # multi-token decode GEMV (T tokens against one weight read: speculative verification), gate/up matrix
+        N, K, W, copies, aq1, asc1, absum1, C1 = mats[0]
+        mt = {}
+        for T in (2, 4, 8):
+            xT = torch.from_numpy(F.synth_activations(T, K, seed=7 + T)).to(dev)
+            aqT, ascT, absT = qm.quantize_act(xT, M_stride=16)
+            CT = torch.empty((T, N), device=dev)
+
+            def oneT(i, aqT=aqT, ascT=ascT, absT=absT, CT=CT, T=T):
+                qm.gemv(copies[i % len(copies)], aqT, ascT, absT, T=T, C=CT, ldc=N)
+            msT = timed_graph(oneT)
+            b = F.weight_bytes(F.IQ4_XS, N, K)
+            mt[str(T)] = {"us_per_launch": round(msT * 1e3, 2), "weight_GB/s": round(b / (msT * 1e-3) / 1e9, 1)}
+        out["gemv_multi_token_5120->17408"] = mt
         # dominant kernel: the gate/up matrix (K 5120 -> N 17408)
         gu = per["5120->17408"]
         traffic = profile_traffic("gemv_iq4_xs_5120x17408")
