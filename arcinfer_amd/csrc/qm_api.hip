@@ -80,13 +80,12 @@ struct MoeLayout {
   int slots, max_tiles, tile_rows;
 };
 
-constexpr int kMoeTileRows = 32;
 
 MoeLayout moe_layout(int T, int NE, int NU, int E, int F) {
   MoeLayout L;
   L.slots = T * NU;
-  L.tile_rows = kMoeTileRows;
-  L.max_tiles = (L.slots + kMoeTileRows - 1) / kMoeTileRows + NE;
+  L.tile_rows = qm::kMoeTileRows;
+  L.max_tiles = (L.slots + qm::kMoeTileRows - 1) / qm::kMoeTileRows + NE;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -394,7 +393,7 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   hipError_t e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
   if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
   if (e == hipSuccess) e = qm::launch_moe_scan(counts, cursor, tstart, tiles, NE, L.tile_rows, s);
-  if (e == hipSuccess) e = qm::launch_moe_scatter(ids, wts, L.slots, NU, cursor, stok, swt, inv, s);
+  if (e == hipSuccess) e = qm::launch_moe_scatter(ids, wts, L.slots, NU, NE, cursor, stok, swt, inv, s);
   if (e == hipSuccess) {
     qm::GemmArgs a{};
     a.w = gate->view;

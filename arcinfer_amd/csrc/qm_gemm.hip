@@ -177,11 +177,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     nvalid = min(BM, a.M - m0);
     wrow0 = 0;
   } else {
-    const int t = blockIdx.y;
+    // a tile of kMoeTileRows slots is split over kMoeTileRows / BM work-groups
+    constexpr int SUB = kMoeTileRows / BM;
+    const int t = blockIdx.y / SUB, sub = blockIdx.y % SUB;
     if (t >= a.tiles[0]) return;
     const int e = a.tiles[1 + 3 * t];
-    m0 = a.tiles[2 + 3 * t];
-    nvalid = a.tiles[3 + 3 * t];
+    m0 = a.tiles[2 + 3 * t] + sub * BM;
+    nvalid = min(BM, a.tiles[3 + 3 * t] - sub * BM);
+    if (nvalid <= 0) return;
     wrow0 = e * a.expert_rows;
     nt = blockIdx.x;
   }
@@ -415,7 +418,8 @@ template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go(const GemmArgs& a, hipStream_t s) {
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
   const unsigned gx = (unsigned)((n_rows + 127) / 128);
-  const unsigned gy = MODE == GEMM_DENSE ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT)) : (unsigned)a.max_tiles;
+  const unsigned gy = MODE == GEMM_DENSE ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT))
+                                          : (unsigned)(a.max_tiles * (kMoeTileRows / (32 * MT)));
   gemm_kernel<TYPE, MT, MODE, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }

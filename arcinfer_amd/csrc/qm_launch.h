@@ -50,13 +50,15 @@ struct GemmArgs {
 };
 enum GemmMode : int { GEMM_DENSE = 0, GEMM_MOE_GATEUP = 1, GEMM_MOE_DOWN = 2 };
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
+// slots per MoE tile (one expert each); a 64-row tile (fewer, larger tiles) measured slower under the Zipf skew
+constexpr int kMoeTileRows = 32;
 
 // MoE routing (qm_moe.hip)
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
                             hipStream_t s);
 hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s);
-hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int* cursor, int* stok, float* swt,
-                              int* inv, hipStream_t s);
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int NE, int* cursor, int* stok,
+                              float* swt, int* inv, hipStream_t s);
 hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
                               hipStream_t s);
 hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s);

@@ -5,66 +5,82 @@
 
 namespace qm {
 
-// One wave per token: the top NU of the NE logits by repeated arg-max (ties: the lower expert), weights
-// exp(l - max) / sum over the selection (summed in selection order), per-expert counts.
+// One wave per token (each wave walks tpw tokens): the top NU of the NE logits by repeated arg-max (ties: the lower
+// expert), weights exp(l - max) / sum over the selection (summed in selection order). Per-expert counts go through
+// a work-group histogram in LDS and one global atomic per (work-group, expert), not one per (token, k): the router's
+// skew (Zipf) would otherwise serialise thousands of atomics on the popular experts' counters.
 // zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of 16-lane sub-groups.
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int ldl, int T, int NE, int NU,
-                                                    int* __restrict__ ids, float* __restrict__ wts,
+                                                    int tpw, int* __restrict__ ids, float* __restrict__ wts,
                                                     int* __restrict__ counts) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  const float* lg = logits + (size_t)t * ldl;
-  float v[PER_LANE];
-  float mx = -INFINITY;
+  __shared__ int hist[64 * PER_LANE];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (counts)
+    for (int e = threadIdx.x; e < NE; e += 256) hist[e] = 0;
+  __syncthreads();
+  for (int j = 0; j < tpw; ++j) {
+    const int t = (blockIdx.x * 4 + wave) * tpw + j;
+    if (t >= T) break;
+    const float* lg = logits + (size_t)t * ldl;
+    float v[PER_LANE];
+    float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < PER_LANE; ++i) {
-    const int e = i * 64 + lane;
-    v[i] = e < NE ? lg[e] : -INFINITY;
-    mx = fmaxf(mx, v[i]);
-  }
+    for (int i = 0; i < PER_LANE; ++i) {
+      const int e = i * 64 + lane;
+      v[i] = e < NE ? lg[e] : -INFINITY;
+      mx = fmaxf(mx, v[i]);
+    }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  float sum = 0.0f, my_p = 0.0f;
-  int my_e = 0;
-  for (int k = 0; k < NU; ++k) {
-    float bv = -INFINITY;
-    int bi = NE;
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sum = 0.0f, my_p = 0.0f;
+    int my_e = 0;
+    for (int k = 0; k < NU; ++k) {
+      float bv = -INFINITY;
+      int bi = NE;
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i)
-      if (v[i] > bv) {
-        bv = v[i];
-        bi = i * 64 + lane;
+      for (int i = 0; i < PER_LANE; ++i)
+        if (v[i] > bv) {
+          bv = v[i];
+          bi = i * 64 + lane;
+        }
+      float gv = bv;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
+      int gi = (bv == gv && bi < NE) ? bi : NE;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i)
+        if (i * 64 + lane == gi) v[i] = -INFINITY;
+      const float p = expf(gv - mx);
+      sum += p;
+      if (lane == k) {
+        my_p = p;
+        my_e = gi;
       }
-    float gv = bv;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
-    int gi = (bv == gv && bi < NE) ? bi : NE;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
-#pragma unroll
-    for (int i = 0; i < PER_LANE; ++i)
-      if (i * 64 + lane == gi) v[i] = -INFINITY;
-    const float p = expf(gv - mx);
-    sum += p;
-    if (lane == k) {
-      my_p = p;
-      my_e = gi;
+    }
+    if (lane < NU) {
+      ids[(size_t)t * NU + lane] = my_e;
+      wts[(size_t)t * NU + lane] = my_p / sum;
+      if (counts) atomicAdd(&hist[my_e], 1);
     }
   }
-  if (lane < NU) {
-    ids[(size_t)t * NU + lane] = my_e;
-    wts[(size_t)t * NU + lane] = my_p / sum;
-    if (counts) atomicAdd(&counts[my_e], 1);
+  if (counts) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < NE; e += 256)
+      if (hist[e]) atomicAdd(&counts[e], hist[e]);
   }
 }
 
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
                             hipStream_t s) {
-  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
-  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
-  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
-  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, ids, wts, counts);
+  // tokens per wave: enough work-groups to cover the CUs (about 1024 waves), more tokens each for large T
+  const int tpw = T >= 2048 ? min(16, T / 1024) : 1;
+  const dim3 grid((unsigned)((T + 4 * tpw - 1) / (4 * tpw))), block(256);
+  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
+  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
+  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
   return hipGetLastError();
 }
 
@@ -111,22 +127,34 @@ hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, in
 }
 
 // Every (token, k) pair takes the next slot of its expert: slot order within an expert is arbitrary, so every
-// consumer works per slot and the combine reads the slots back through inv in k order.
+// consumer works per slot and the combine reads the slots back through inv in k order. A work-group ranks its 256
+// pairs per expert in LDS, reserves each expert's range with one global atomic, then writes the slots.
 // zero/kernels/moe.cl:163-171 (moe_scatter).
 __global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ ids, const float* __restrict__ wts, int n,
-                                                      int NU, int* __restrict__ cursor, int* __restrict__ stok,
+                                                      int NU, int NE, int* __restrict__ cursor, int* __restrict__ stok,
                                                       float* __restrict__ swt, int* __restrict__ inv) {
+  extern __shared__ int sh[];
+  int* cnt = sh;        // [NE] pairs of this work-group per expert
+  int* base = sh + NE;  // [NE] first slot reserved for them
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  for (int e = threadIdx.x; e < NE; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  const int e = i < n ? ids[i] : 0;
+  const int r = i < n ? atomicAdd(&cnt[e], 1) : 0;
+  __syncthreads();
+  for (int x = threadIdx.x; x < NE; x += blockDim.x)
+    if (cnt[x]) base[x] = atomicAdd(&cursor[x], cnt[x]);
+  __syncthreads();
   if (i >= n) return;
-  const int slot = atomicAdd(&cursor[ids[i]], 1);
+  const int slot = base[e] + r;
   stok[slot] = i / NU;
   swt[slot] = wts[i];
   inv[i] = slot;
 }
 
-hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int* cursor, int* stok, float* swt,
-                              int* inv, hipStream_t s) {
-  scatter_kernel<<<(n + 255) / 256, 256, 0, s>>>(ids, wts, n, NU, cursor, stok, swt, inv);
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int NE, int* cursor, int* stok,
+                              float* swt, int* inv, hipStream_t s) {
+  scatter_kernel<<<(n + 255) / 256, 256, 2 * sizeof(int) * NE, s>>>(ids, wts, n, NU, NE, cursor, stok, swt, inv);
   return hipGetLastError();
 }
 
