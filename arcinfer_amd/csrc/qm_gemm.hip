@@ -308,6 +308,38 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
           pay2[b] = load_payload<TYPE>(a.w2, n, sn * 8 + b, hf);
         }
       }
+      if constexpr (MODE == GEMM_DENSE && !DUMP && MT == 2) {
+        // both row tiles' MFMAs first, then the epilogues: row tile 0's VALU epilogue runs while row tile 1's
+        // MFMAs execute, and row tile 1's epilogue while row tile 0's mins MFMA does
+        v16i dv[2][2];
+        v32f sc[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const uint4 av = *(const uint4*)(L.a[cur] + (mt * 32 + lc) * A_STRIDE + 32 * (2 * p + q) + 16 * hf);
+            const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+            dv[mt][q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[q], zero16, 0, 0, 0);
+          }
+          const float my_asc = L.asc[cur][(2 * p + hf) * BM + mt * 32 + lc];
+          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            acc[mt][r] = fmaf(sc[mt][r], (float)dv[mt][0][r], acc[mt][r]);
+            acc[mt][r] = fmaf(sc[mt][16 + r], (float)dv[mt][1][r], acc[mt][r]);
+          }
+          if constexpr (MINS) {
+            const float my_u = L.u[cur][(2 * p + hf) * BM + mt * 32 + lc];
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(my_u, my_dmn, acc[mt], 0, 0, 0);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
+          }
+        }
+      } else
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         v16i dv[2], dv2[2];
