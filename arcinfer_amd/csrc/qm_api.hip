@@ -217,6 +217,53 @@ int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, in
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_quantize_act");
 }
 
+static int check_out_acts(const char* fn, int M, int M_stride, int K, const int8_t* aq, const float* asc,
+                          const int16_t* absum) {
+  if (!aq || !asc || !absum) return fail(QM_ERR_ARG, "%s: null output pointer", fn);
+  if (K <= 0 || K % 32 || M < 0 || M_stride < 1 || M > M_stride)
+    return fail(QM_ERR_SHAPE, "%s: M %d, M_stride %d, K %d", fn, M, M_stride, K);
+  if (!aligned(aq, 4)) return fail(QM_ERR_ARG, "%s: aq must be 4-byte aligned", fn);
+  return QM_OK;
+}
+
+int qmatmul_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
+                          float* asc, int16_t* absum, float* h, int ldh, void* stream) {
+  if (int st = check_out_acts("qmatmul_rmsnorm_quant", M, M_stride, K, aq, asc, absum)) return st;
+  if (!x || !w) return fail(QM_ERR_ARG, "qmatmul_rmsnorm_quant: null input");
+  if (ldx < K || ldx % 4 || !aligned(x, 16) || !aligned(w, 16) || (h && (ldh < K || ldh % 4 || !aligned(h, 16))))
+    return fail(QM_ERR_ARG, "qmatmul_rmsnorm_quant: x, w, h need 16-byte aligned rows (ldx %d, ldh %d, K %d)", ldx,
+                ldh, K);
+  QM_CHECK_INIT();
+  const hipError_t e = qm::launch_rmsnorm_quant(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh,
+                                                (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_rmsnorm_quant");
+}
+
+int qmatmul_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                         float* asc, int16_t* absum, void* stream) {
+  if (int st = check_out_acts("qmatmul_swiglu_quant", M, M_stride, F, aq, asc, absum)) return st;
+  if (!gu) return fail(QM_ERR_ARG, "qmatmul_swiglu_quant: null input");
+  if (ldg < (fused ? F : 2 * F) || ldg % 4 || !aligned(gu, 16))
+    return fail(QM_ERR_ARG, "qmatmul_swiglu_quant: ldg %d for F %d (fused %d), 16-byte aligned rows", ldg, F, fused);
+  QM_CHECK_INIT();
+  const hipError_t e = qm::launch_swiglu_quant(gu, ldg, F, M, M_stride, fused ? 1 : 0, gelu ? 1 : 0, aq, asc, absum,
+                                               (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_swiglu_quant");
+}
+
+int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
+                           int M_stride, int8_t* aq, float* asc, int16_t* absum, void* stream) {
+  if (int st = check_out_acts("qmatmul_add_norm_quant", M, M_stride, K, aq, asc, absum)) return st;
+  if (!x || !t || !w) return fail(QM_ERR_ARG, "qmatmul_add_norm_quant: null input");
+  if (K > 16384) return fail(QM_ERR_SHAPE, "qmatmul_add_norm_quant: K %d (at most 16384)", K);
+  if (!aligned(x, 16) || !aligned(t, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16)))
+    return fail(QM_ERR_ARG, "qmatmul_add_norm_quant: x, t, w, w2 must be 16-byte aligned");
+  QM_CHECK_INIT();
+  const hipError_t e = qm::launch_add_norm_quant(x, t, w, K, eps, s, w2, M, M_stride, aq, asc, absum,
+                                                 (hipStream_t)stream);
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_add_norm_quant");
+}
+
 static int check_acts(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
                       int rows_needed, int M_stride) {
   if (!w || !aq || !asc) return fail(QM_ERR_ARG, "%s: null pointer", fn);

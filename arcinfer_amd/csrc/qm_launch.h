@@ -53,6 +53,15 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
 // slots per MoE tile (one expert each); a 64-row tile (fewer, larger tiles) measured slower under the Zipf skew
 constexpr int kMoeTileRows = 32;
 
+// Activation producers (qm_producers.hip)
+hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps,
+                                int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, hipStream_t s);
+hipError_t launch_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                               float* asc, int16_t* absum, hipStream_t s);
+hipError_t launch_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float scale,
+                                 const float* w2, int M, int M_stride, int8_t* aq, float* asc, int16_t* absum,
+                                 hipStream_t s);
+
 // MoE routing (qm_moe.hip)
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
                             hipStream_t s);

@@ -35,6 +35,9 @@ SIGNATURES = [
     ("qmatmul_moe_ws_layout", _I, [_I, _I, _I, _I, _I, _P]),
     ("qmatmul_gemv_blocksums", _I, [_P, _P, _P, _I, _I, _P, _P, _P]),
     ("qmatmul_gemm_blocksums", _I, [_P, _P, _I, _I, _P, _P]),
+    ("qmatmul_rmsnorm_quant", _I, [_P, _I, _P, _I, _I, _I, _c.c_float, _P, _P, _P, _P, _I, _P]),
+    ("qmatmul_swiglu_quant", _I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_add_norm_quant", _I, [_P, _P, _P, _I, _c.c_float, _c.c_float, _P, _I, _I, _P, _P, _P, _P]),
 ]
 
 
@@ -213,3 +216,40 @@ def moe_grouped(gate, up, down, NE, logits, NU, aq, asc, x, ws, T=None, accumula
     _call("qmatmul_moe_grouped", gate.handle, up.handle, down.handle, NE, _ptr(logits), logits.stride(0), T, NU,
           _ptr(aq), _ptr(asc), aq.shape[0], _ptr(x), accumulate, _ptr(ws), ws.numel(), _stream(stream))
     return x
+
+
+def _out_acts(Ms, K, dev):
+    import torch
+    return (torch.empty((Ms, K), dtype=torch.int8, device=dev), torch.empty((K // 32, Ms), dtype=torch.float32, device=dev),
+            torch.empty((K // 16, Ms), dtype=torch.int16, device=dev))
+
+
+def rmsnorm_quant(x, w, eps, M_stride=None, want_h=False, stream=None):
+    """x f32 [M, K] (cuda), w [K] -> (aq, asc, absum, h or None)."""
+    import torch
+    M, K = x.shape
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum = _out_acts(Ms, K, x.device)
+    h = torch.empty((Ms, K), dtype=torch.float32, device=x.device) if want_h else None
+    _call("qmatmul_rmsnorm_quant", _ptr(x), x.stride(0), _ptr(w), K, M, Ms, float(eps), _ptr(aq), _ptr(asc),
+          _ptr(absum), _ptr(h), K, _stream(stream))
+    return aq, asc, absum, h
+
+
+def swiglu_quant(gu, F, fused=False, gelu=False, M_stride=None, stream=None):
+    M = gu.shape[0]
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum = _out_acts(Ms, F, gu.device)
+    _call("qmatmul_swiglu_quant", _ptr(gu), gu.stride(0), F, M, Ms, int(fused), int(gelu), _ptr(aq), _ptr(asc),
+          _ptr(absum), _stream(stream))
+    return aq, asc, absum
+
+
+def add_norm_quant(x, t, w, eps, s, w2=None, M_stride=None, stream=None):
+    """Updates x in place; returns (aq, asc, absum)."""
+    M, K = x.shape
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum = _out_acts(Ms, K, x.device)
+    _call("qmatmul_add_norm_quant", _ptr(x), _ptr(t), _ptr(w), K, float(eps), float(s), _ptr(w2), M, Ms, _ptr(aq),
+          _ptr(asc), _ptr(absum), _stream(stream))
+    return aq, asc, absum

@@ -78,6 +78,26 @@ int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K);
 int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
                          void* stream);
 
+/* Producers of the activations (the step before every product), fused with the quantizer above (act32 layout):
+ *
+ * qmatmul_rmsnorm_quant: y[m] = x[m] * r * w, r = 1 / sqrt(mean(x[m]^2) + eps), quantized; rows M..M_stride-1 zero.
+ *   h (optional, row stride ldh) receives y. Replaces the rmsnorm_quant kernel (zero/kernels/ops.cl:82-104, launched
+ *   by Engine::rmsnorm_quant, zero/engine.h:3302-3308); its row_off is a pointer offset on x here.
+ * qmatmul_swiglu_quant: y[m] = silu(gate) * up (gelu_tanh(gate) * up with gelu) from rows [gate(F) | up(F)] of stride
+ *   ldg, or y[m] = the row itself with fused (the engine's quant_rows), quantized. Replaces swiglu_quant
+ *   (ops.cl:110-128; zero/engine.h:3451-3456).
+ * qmatmul_add_norm_quant: x[m] = (x[m] + t[m] * r * w) * s (r from t[m]'s mean square; x updated in place), then
+ *   y[m] = x[m] * r2 * w2 (r2 from the new x[m]) or, with w2 == NULL, y[m] = x[m]; y quantized. Rows of stride K,
+ *   K <= 16384. Replaces add_norm_quant (ops.cl:2025-2075; zero/engine.h:3415).
+ * Sums of squares are f32, so y matches a CPU evaluation to float tolerance, not bit for bit; the quantization of y
+ * is the quantizer's exact arithmetic. Pointers to f32 rows must be 16-byte aligned with row strides % 4 == 0. */
+int qmatmul_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
+                          float* asc, int16_t* absum, float* h, int ldh, void* stream);
+int qmatmul_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                         float* asc, int16_t* absum, void* stream);
+int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
+                           int M_stride, int8_t* aq, float* asc, int16_t* absum, void* stream);
+
 /* Decode GEMV, T tokens (1..8) against one read of the weight:
  *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
  * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K only.

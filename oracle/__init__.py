@@ -15,6 +15,9 @@ Pinning (each function is checked by something other than a retyped formula; tes
   matmul_f32                  numpy float64 matmul of the dequantized rows
   moe_route                   textbook stable-sort top-k and softmax over the selection (tests/test_route.cpp recipe)
   moe_forward                 a numpy pipeline built from the pinned pieces (route, blockdot, quantize_act)
+  rmsnorm_quant / swiglu_quant / add_norm_quant
+                              closed forms (constant rows, zero rows, t = 0, silu/gelu limits and identities), float64
+                              references of the norms, and the pinned quantizer on the returned f32 values
 """
 import ctypes
 import os
@@ -55,6 +58,13 @@ def lib():
         _lib.qref_moe_route.argtypes = [P, I, I, I, I, P, P, P]
         _lib.qref_moe_route.restype = None
         _lib.qref_moe_forward.argtypes = [I, P, I, P, I, P, I, I, I, P, I, I, I, P, P, I, P, I, I]
+        Fl = ctypes.c_float
+        _lib.qref_rmsnorm_quant.argtypes = [P, I, P, I, I, I, Fl, P, P, P, P]
+        _lib.qref_rmsnorm_quant.restype = None
+        _lib.qref_swiglu_quant.argtypes = [P, I, I, I, I, I, I, P, P, P, P]
+        _lib.qref_swiglu_quant.restype = None
+        _lib.qref_add_norm_quant.argtypes = [P, P, P, I, Fl, Fl, P, I, I, P, P, P, P]
+        _lib.qref_add_norm_quant.restype = None
     return _lib
 
 
@@ -167,3 +177,43 @@ def moe_forward(tg, Wg, tu, Wu, td, Wd, NE, E, F, logits, NU, aq, asc, x=None, a
                               _p(aq), _p(asc), aq.shape[0], _p(out), 1 if accumulate else 0, nthreads):
         raise ValueError("moe_forward failed")
     return out
+
+
+def _acts(Ms, K):
+    return (np.zeros((Ms, K), dtype=np.int8), np.zeros((K // 32, Ms), dtype=np.float32),
+            np.zeros((K // 16, Ms), dtype=np.int16), np.zeros((Ms, K), dtype=np.float32))
+
+
+def rmsnorm_quant(x, w, eps, M_stride=None):
+    """x f32 [M, K] (row stride K), w [K] -> (aq, asc, absum, h) (zero rows M..M_stride-1)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, K = x.shape
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum, h = _acts(Ms, K)
+    lib().qref_rmsnorm_quant(_p(x), K, _p(w), K, M, Ms, float(eps), _p(aq), _p(asc), _p(absum), _p(h))
+    return aq, asc, absum, h
+
+
+def swiglu_quant(gu, F, fused=False, gelu=False, M_stride=None):
+    """gu f32 [M, 2F] ([gate | up]) or [M, F] with fused -> (aq, asc, absum, h)."""
+    gu = np.ascontiguousarray(gu, dtype=np.float32)
+    M, ldg = gu.shape
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum, h = _acts(Ms, F)
+    lib().qref_swiglu_quant(_p(gu), ldg, F, M, Ms, int(fused), int(gelu), _p(aq), _p(asc), _p(absum), _p(h))
+    return aq, asc, absum, h
+
+
+def add_norm_quant(x, t, w, eps, s, w2=None, M_stride=None):
+    """Returns (x_new, aq, asc, absum, h); x is not modified."""
+    xn = np.ascontiguousarray(x, dtype=np.float32).copy()
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    w2 = None if w2 is None else np.ascontiguousarray(w2, dtype=np.float32)
+    M, K = xn.shape
+    Ms = M if M_stride is None else M_stride
+    aq, asc, absum, h = _acts(Ms, K)
+    lib().qref_add_norm_quant(_p(xn), _p(t), _p(w), K, float(eps), float(s), _p(w2), M, Ms, _p(aq), _p(asc),
+                              _p(absum), _p(h))
+    return xn, aq, asc, absum, h

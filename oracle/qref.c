@@ -414,3 +414,70 @@ int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_
   free(wts);
   return 0;
 }
+
+/* ---- activation producers: the kernels that write the path's int8 activations --------------------------------- */
+
+static double sumsq_f64(const float* v, int K) {
+  double ss = 0.0;
+  for (int i = 0; i < K; ++i) ss += (double)v[i] * (double)v[i];
+  return ss;
+}
+
+/* zero/kernels/ops.cl:82-104 (rmsnorm_quant, act32): y = x * r * w with r = 1 / sqrt(ss / K + eps), ss = sum of x^2
+ * (accumulated in double here; the GPU kernels sum in f32, in their own order), then quantized per 32 as
+ * quant_store16 (ops.cl:18-77). Rows M..M_stride-1 are zero rows (the reference's `valid` flag). h (optional, row
+ * stride K) receives y, zero rows included. */
+void qref_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
+                        float* asc, int16_t* absum, float* h) {
+  float* y = (float*)calloc((size_t)M_stride * K, sizeof(float));
+  for (int m = 0; m < M; ++m) {
+    const float* xr = x + (size_t)m * ldx;
+    const float ss = (float)sumsq_f64(xr, K);
+    const float r = 1.0f / sqrtf(ss / (float)K + eps);
+    for (int i = 0; i < K; ++i) y[(size_t)m * K + i] = xr[i] * r * w[i];
+  }
+  qref_quantize_act(y, M, K, M_stride, 1, aq, asc, absum);
+  if (h) memcpy(h, y, sizeof(float) * (size_t)M_stride * K);
+  free(y);
+}
+
+/* ops.cl:13 (silu) and 107 (gelu_tanh) */
+static float silu_f(float x) { return x / (1.0f + expf(-x)); }
+static float gelu_tanh_f(float x) {
+  return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+}
+
+/* ops.cl:110-128 (swiglu_quant, act32): y = silu(gate) * up (gelu_tanh with `gelu`) from rows [gate(F) | up(F)], or
+ * with `fused` the row itself (the GEMM already applied the activation: the engine's quant_rows, engine.h:3451-3456),
+ * quantized per 32. Row stride ldg. */
+void qref_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                       float* asc, int16_t* absum, float* h) {
+  float* y = (float*)calloc((size_t)M_stride * F, sizeof(float));
+  for (int m = 0; m < M; ++m) {
+    const float* g = gu + (size_t)m * ldg;
+    for (int i = 0; i < F; ++i)
+      y[(size_t)m * F + i] = fused ? g[i] : (gelu ? gelu_tanh_f(g[i]) : silu_f(g[i])) * g[F + i];
+  }
+  qref_quantize_act(y, M, F, M_stride, 1, aq, asc, absum);
+  if (h) memcpy(h, y, sizeof(float) * (size_t)M_stride * F);
+  free(y);
+}
+
+/* ops.cl:2025-2075 (add_norm_quant, act32): per row, x = (x + t * r * w) * s with r from t's mean square, written
+ * back to x; then y = x * r2 * w2 (r2 from the new x's mean square) or, with w2 == NULL, y = x; y quantized per 32.
+ * x and t rows have stride K. */
+void qref_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
+                         int M_stride, int8_t* aq, float* asc, int16_t* absum, float* h) {
+  float* y = (float*)calloc((size_t)M_stride * K, sizeof(float));
+  for (int m = 0; m < M; ++m) {
+    float* xr = x + (size_t)m * K;
+    const float* tr = t + (size_t)m * K;
+    const float r = 1.0f / sqrtf((float)sumsq_f64(tr, K) / (float)K + eps);
+    for (int i = 0; i < K; ++i) xr[i] = (xr[i] + tr[i] * r * w[i]) * s;
+    const float r2 = w2 ? 1.0f / sqrtf((float)sumsq_f64(xr, K) / (float)K + eps) : 1.0f;
+    for (int i = 0; i < K; ++i) y[(size_t)m * K + i] = w2 ? xr[i] * r2 * w2[i] : xr[i];
+  }
+  qref_quantize_act(y, M, K, M_stride, 1, aq, asc, absum);
+  if (h) memcpy(h, y, sizeof(float) * (size_t)M_stride * K);
+  free(y);
+}

@@ -59,6 +59,15 @@ int qref_blockdot(int type, const uint8_t* W, int N, int K, const int8_t* aq, co
 int qref_matmul_f32(int type, const uint8_t* W, int N, int K, const float* X, int M, float* Y, int nthreads);
 
 /* routing (moe.cl:42-81): top NU of the logits (ties: lower expert), w = exp(l - max) / sum over the selection */
+/* Activation producers (zero/kernels/ops.cl:82-128, 2025-2075), act32 layout; h (optional) receives the f32 values
+ * that were quantized, [M_stride][K]. */
+void qref_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
+                        float* asc, int16_t* absum, float* h);
+void qref_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                       float* asc, int16_t* absum, float* h);
+void qref_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
+                         int M_stride, int8_t* aq, float* asc, int16_t* absum, float* h);
+
 void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts);
 
 /* full MoE FFN on the int8 path (engine_moe.h:8-282, moe.cl:251-340):
