@@ -11,7 +11,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqmatmul.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemm.hip", "qm_moe.hip", "qm_producers.hip", "qm_api.hip"]
+SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemm.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt",

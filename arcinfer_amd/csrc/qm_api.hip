@@ -1,5 +1,6 @@
 // The C ABI of include/qmatmul.h: argument and shape checks, weight preparation, workspace layout, launches.
 // Never throws or exits; errors come back as qm_status with a message in qmatmul_last_error().
+#include <stdlib.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -76,7 +77,7 @@ int ensure_init() {
   } while (0)
 
 struct MoeLayout {
-  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, total;
+  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, hf, total;
   int slots, max_tiles, tile_rows;
 };
 
@@ -104,6 +105,7 @@ MoeLayout moe_layout(int T, int NE, int NU, int E, int F) {
   L.hq = take((size_t)L.slots * F);
   L.hsc = take(sizeof(float) * (size_t)(F / 32) * L.slots);
   L.y = take(sizeof(float) * (size_t)L.slots * E);
+  L.hf = take(sizeof(float) * (size_t)L.slots * F);
   L.total = o;
   return L;
 }
@@ -378,6 +380,7 @@ int qmatmul_moe_ws_layout(int T, int NE, int NU, int E, int F, qm_moe_ws_layout*
   out->hq = L.hq;
   out->hsc = L.hsc;
   out->y = L.y;
+  out->hf = L.hf;
   out->total = L.total;
   out->slots = L.slots;
   out->max_tiles = L.max_tiles;
@@ -437,6 +440,15 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   int8_t* hq = (int8_t*)(b + L.hq);
   float* hsc = (float*)(b + L.hsc);
   float* y = (float*)(b + L.y);
+  // decode sizes: GEMV-shaped expert kernels (no tiles, no scatter), one launch each for route, gate/up, down
+  static const int dec_env = getenv("QM_MOE_DECODE") ? atoi(getenv("QM_MOE_DECODE")) : 1;
+  if (dec_env && T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192 && down->type == gate->type) {
+    hipError_t e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, nullptr, s);
+    if (e == hipSuccess)
+      e = qm::launch_moe_decode(gate->type, gate->view, up->view, down->view, T, NU, E, F, ids, wts, aq, asc, M_stride,
+                                (float*)(b + L.hf), x, accumulate, s);
+    return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
+  }
   hipError_t e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
   if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
   if (e == hipSuccess) e = qm::launch_moe_scan(counts, cursor, tstart, tiles, NE, L.tile_rows, s);

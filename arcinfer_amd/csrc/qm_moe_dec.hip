@@ -1,0 +1,203 @@
+// MoE FFN at decode sizes (a few tokens): GEMV-shaped kernels instead of expert-grouped GEMM tiles, the role of the
+// reference's per-tile moe_gateup_q / moe_down_q (zero/kernels/decode.cl:1500-1847). Same arithmetic as the tile
+// path: h = up * silu(gate) per expert row, h quantized per 32 (moe.cl:251-282), down times the routing weight, and
+// the token's NU expert outputs summed in selection order (moe.cl:332-340).
+#include "qm_decode.h"
+
+namespace qm {
+
+namespace {
+
+template <int TYPE>
+__device__ __forceinline__ int block_isum(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int b,
+                                          const KvTab& kv, const uint8_t* sq, int nb, float& d) {
+  uint32_t wd[8];
+  int sc, mn;
+  float dmin;
+  decode_block32<TYPE>(r, lds, b & 7, kv, wd, sc, mn, d, dmin);
+  const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
+  int isum = dot4(x0.x, wd[0], 0);
+  isum = dot4(x0.y, wd[1], isum);
+  isum = dot4(x0.z, wd[2], isum);
+  isum = dot4(x0.w, wd[3], isum);
+  isum = dot4(x1.x, wd[4], isum);
+  isum = dot4(x1.y, wd[5], isum);
+  isum = dot4(x1.z, wd[6], isum);
+  isum = dot4(x1.w, wd[7], isum);
+  return __mul24(sc, isum);
+}
+
+}  // namespace
+
+// Gate/up: grid (slots, F / 8). A work-group stages its token's int8 row in LDS (two 16-byte planes per 32-block, as
+// the decode GEMV) and its 8 lane groups of 32 take one expert row j each: g = gate_e[j] . a_t, u = up_e[j] . a_t,
+// h[slot][j] = u * silu(g). CH = ceil(E / 1024) blocks per lane.
+template <int TYPE, int CH>
+__global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView up, const int* __restrict__ ids, int NU,
+                                                             int F, const int8_t* __restrict__ aq,
+                                                             const float* __restrict__ asc, int M_stride,
+                                                             float* __restrict__ h) {
+  extern __shared__ uint4 smem[];
+  __shared__ typename LdsFor<TYPE>::type lds;
+  using Tr = Traits<TYPE>;
+  const int E = gate.K, nb = E / 32;
+  uint8_t* sq = (uint8_t*)smem;
+  float* ssc = (float*)(sq + (size_t)E);
+  const int slot = blockIdx.x, t = slot / NU, e = ids[slot];
+  const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
+  const int j = min((int)blockIdx.y * 8 + grp, F - 1);
+  const size_t row = (size_t)e * F + j;
+  RawBlk rg[CH], ru[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int b = min(gl + 32 * u, nb - 1);
+    rg[u] = load_block_at<TYPE>(gate.qs + row * nb * Tr::QB, gate.hdr + row * (nb / 8) * Tr::HB, b);
+    ru[u] = load_block_at<TYPE>(up.qs + row * nb * Tr::QB, up.hdr + row * (nb / 8) * Tr::HB, b);
+  }
+  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
+    const int b = i >> 1, hh = i & 1;
+    *(uint4*)(sq + (size_t)hh * nb * 16 + b * 16) = *(const uint4*)(aq + (size_t)t * E + 32 * b + 16 * hh);
+  }
+  for (int b = threadIdx.x; b < nb; b += 256) ssc[b] = asc[(size_t)b * M_stride + t];
+  __syncthreads();
+  const KvTab kv = kv_tab();
+  float g = 0.0f, uu = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int b = gl + 32 * u;
+    if (b < nb) {
+      float d;
+      const int ig = block_isum<TYPE>(rg[u], &lds, b, kv, sq, nb, d);
+      g += ssc[b] * d * (float)ig;
+      const int iu = block_isum<TYPE>(ru[u], &lds, b, kv, sq, nb, d);
+      uu += ssc[b] * d * (float)iu;
+    }
+  }
+  g = wave_sum_width(g, 32);
+  uu = wave_sum_width(uu, 32);
+  if (gl == 0 && (int)blockIdx.y * 8 + grp < F) h[(size_t)slot * F + j] = uu * (g / (1.0f + expf(-g)));
+}
+
+// Down + combine: grid (T, ceil(E / GPW)). The work-group quantizes its token's NU rows of h per 32 into LDS (two
+// planes per row, as the activations of the decode GEMV), then each lane group of LPR lanes takes one output column c:
+// for k = 0..NU-1, y_k = w_k * (down_{e_k}[c] . q(h_k)), summed in k order; x[t][c] (+)= the sum. The NU expert rows
+// of a column are loaded before any is decoded. F / 32 <= LPR * CH, NU <= 8.
+template <int TYPE, int LPR, int CH>
+__global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, const int* __restrict__ ids,
+                                                           const float* __restrict__ wts, int NU,
+                                                           const float* __restrict__ h, float* __restrict__ x,
+                                                           int accumulate) {
+  extern __shared__ uint4 smem[];
+  __shared__ typename LdsFor<TYPE>::type lds;
+  using Tr = Traits<TYPE>;
+  constexpr int GPW = 256 / LPR, NUMAX = 8;
+  const int F = down.K, nb = F / 32;
+  uint8_t* sq = (uint8_t*)smem;               // [NU][2][nb][16]
+  float* ssc = (float*)(sq + (size_t)NU * F);  // [NU][nb]
+  const int t = blockIdx.x, grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+  const int c_raw = blockIdx.y * GPW + grp, c = min(c_raw, E - 1);
+  RawBlk r[NUMAX][CH];
+#pragma unroll
+  for (int k = 0; k < NUMAX; ++k)
+    if (k < NU) {
+      const size_t row = (size_t)ids[(size_t)t * NU + k] * E + c;
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        r[k][u] = load_block_at<TYPE>(down.qs + row * nb * Tr::QB, down.hdr + row * (nb / 8) * Tr::HB,
+                                      min(gl + LPR * u, nb - 1));
+    }
+  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  // h rows of the token's NU slots, quantized per 32 (8 lanes per block: the quantizer's arithmetic)
+  for (int b0 = 0; b0 < NU * nb; b0 += 32) {
+    const int bi = b0 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+    const bool live = bi < NU * nb;
+    const int k = live ? bi / nb : 0, b = live ? bi % nb : 0;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+      const float4 hv = *(const float4*)(h + ((size_t)t * NU + k) * F + 32 * b + 4 * sub);
+      v[0] = hv.x;
+      v[1] = hv.y;
+      v[2] = hv.z;
+      v[3] = hv.w;
+    }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t pk = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk |= (uint32_t)((int)__builtin_rintf(v[i] * inv) & 0xFF) << (8 * i);
+    if (live) {
+      *(uint32_t*)(sq + (size_t)k * F + (size_t)(sub >> 2) * nb * 16 + b * 16 + 4 * (sub & 3)) = pk;
+      if (sub == 0) ssc[k * nb + b] = amax / 127.0f;
+    }
+  }
+  __syncthreads();
+  const KvTab kv = kv_tab();
+  float v = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NUMAX; ++k)
+    if (k < NU) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int b = gl + LPR * u;
+        if (b < nb) {
+          float d;
+          const int iv = block_isum<TYPE>(r[k][u], &lds, b, kv, sq + (size_t)k * F, nb, d);
+          acc += ssc[k * nb + b] * d * (float)iv;
+        }
+      }
+      acc = wave_sum_width(acc, LPR);
+      const float y = wts[(size_t)t * NU + k] * acc;
+      v += y;
+    }
+  if (gl == 0 && c_raw < E) {
+    float* xp = x + (size_t)t * E + c;
+    *xp = accumulate ? *xp + v : v;
+  }
+}
+
+template <int TYPE>
+static hipError_t moe_dec_typed(const WView& gate, const WView& up, const WView& down, int T, int NU, int E, int F,
+                                const int* ids, const float* wts, const int8_t* aq, const float* asc, int M_stride,
+                                float* h, float* x, int accumulate, hipStream_t s) {
+  const int slots = T * NU, nbE = E / 32, nbF = F / 32;
+  const size_t shg = (size_t)E + sizeof(float) * nbE;
+  const dim3 gg((unsigned)slots, (unsigned)((F + 7) / 8));
+  switch ((nbE + 31) / 32) {
+    case 1: moe_gateup_dec_kernel<TYPE, 1><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
+    case 2: moe_gateup_dec_kernel<TYPE, 2><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
+    case 3:
+    case 4: moe_gateup_dec_kernel<TYPE, 4><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
+    default: moe_gateup_dec_kernel<TYPE, 8><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t shd = (size_t)NU * F + sizeof(float) * NU * nbF;
+  if (nbF <= 16) {
+    const dim3 gd((unsigned)T, (unsigned)((E + 15) / 16));
+    moe_down_dec_kernel<TYPE, 16, 1><<<gd, 256, shd, s>>>(down, E, ids, wts, NU, h, x, accumulate);
+  } else {
+    const dim3 gd((unsigned)T, (unsigned)((E + 7) / 8));
+    if (nbF <= 32) moe_down_dec_kernel<TYPE, 32, 1><<<gd, 256, shd, s>>>(down, E, ids, wts, NU, h, x, accumulate);
+    else if (nbF <= 64) moe_down_dec_kernel<TYPE, 32, 2><<<gd, 256, shd, s>>>(down, E, ids, wts, NU, h, x, accumulate);
+    else moe_down_dec_kernel<TYPE, 32, 4><<<gd, 256, shd, s>>>(down, E, ids, wts, NU, h, x, accumulate);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const WView& down, int T, int NU, int E,
+                             int F, const int* ids, const float* wts, const int8_t* aq, const float* asc, int M_stride,
+                             float* h, float* x, int accumulate, hipStream_t s) {
+  switch (type) {
+    case T_Q8_0: return moe_dec_typed<T_Q8_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ4_XS: return moe_dec_typed<T_IQ4_XS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ3_S: return moe_dec_typed<T_IQ3_S>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qm

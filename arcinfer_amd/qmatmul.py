@@ -50,7 +50,7 @@ class QMatmulError(RuntimeError):
 class MoeWsLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("ids", "wts", "counts", "cursor", "tstart", "tiles", "stok", "swt", "inv", "hq", "hsc", "y",
-                 "total")] + [("slots", ctypes.c_int), ("max_tiles", ctypes.c_int), ("tile_rows", ctypes.c_int)]
+                 "hf", "total")] + [("slots", ctypes.c_int), ("max_tiles", ctypes.c_int), ("tile_rows", ctypes.c_int)]
 
 
 _lib = None

@@ -58,6 +58,28 @@ def timed(fn, steps, warmup, stream, pre=None):
     return start.elapsed_time(end) / steps, wall
 
 
+def graphed(fn, n):
+    """fn(0..n-1) captured once into a HIP graph (torch.cuda.CUDAGraph on ROCm)."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    return g
+
+
+def timed_graph(fn, args, stream):
+    """W warmup steps, then exactly K timed steps, each captured once and replayed: short launches (a batch-1 GEMV is
+    ~10 us of GPU time, about what a Python-side launch costs) would otherwise time the host."""
+    import torch
+    for i in range(2):
+        fn(i)  # (first-launch work stays out of the captures)
+    torch.cuda.synchronize()
+    gw, gt = graphed(fn, max(1, args.warmup)), graphed(fn, args.steps)
+    ms, _ = timed(lambda i: gt.replay(), 1, 0, stream, pre=gw.replay)
+    return ms / args.steps
+
+
 def profile_traffic(kernel_key):
     """Bytes per launch from the committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, calibrated on a copy
     kernel), or None."""
@@ -115,25 +137,7 @@ def main():
             for N, K, W, copies, aq, asc, absum, C in mats:
                 qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N)
 
-        # The steps as HIP graphs (W warmup steps, then exactly K timed steps, each captured once and replayed): a
-        # batch-1 GEMV launch is ~10 us of GPU time, about what a Python-side launch costs, so eager launches would
-        # time the host.
-        def graphed(fn, n):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                for i in range(n):
-                    fn(i)
-            return g
-
-        def timed_graph(fn):
-            for i in range(2):
-                fn(i)  # (first-launch work stays out of the captures)
-            torch.cuda.synchronize()
-            gw, gt = graphed(fn, max(1, args.warmup)), graphed(fn, args.steps)
-            ms, _ = timed(lambda i: gt.replay(), 1, 0, stream, pre=gw.replay)
-            return ms / args.steps
-
-        ms = timed_graph(step)
+        ms = timed_graph(step, args, stream)
         gbs = bytes_per_step / (ms * 1e-3) / 1e9
         out["value"] = round(gbs, 1)
         out["ms_per_step"] = round(ms, 5)
@@ -142,7 +146,7 @@ def main():
         for N, K, W, copies, aq, asc, absum, C in mats:
             def one(i, copies=copies, aq=aq, asc=asc, absum=absum, C=C, N=N):
                 qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N)
-            ms1 = timed_graph(one)
+            ms1 = timed_graph(one, args, stream)
             b = F.weight_bytes(F.IQ4_XS, N, K)
             per[f"{K}->{N}"] = {"us_per_launch": round(ms1 * 1e3, 2), "GB/s": round(b / (ms1 * 1e-3) / 1e9, 1),
                                "weight_bytes": b}
@@ -157,7 +161,7 @@ def main():
 
             def oneT(i, aqT=aqT, ascT=ascT, absT=absT, CT=CT, T=T):
                 qm.gemv(copies[i % len(copies)], aqT, ascT, absT, T=T, C=CT, ldc=N)
-            msT = timed_graph(oneT)
+            msT = timed_graph(oneT, args, stream)
             b = F.weight_bytes(F.IQ4_XS, N, K)
             mt[str(T)] = {"us_per_launch": round(msT * 1e3, 2), "weight_GB/s": round(b / (msT * 1e-3) / 1e9, 1)}
         out["gemv_multi_token_5120->17408"] = mt
@@ -246,6 +250,19 @@ def main():
                       "expert_weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
                       "config": "256 experts IQ4_XS, E 2048, F 512, T 4096, top-8, Zipf(1.1) router; "
                                 "route + scan + scatter + gate/up + down + combine"}
+        # decode-size MoE (T tokens, each through its 8 experts): latency per call
+        dec = {}
+        for Tq in (1, 4, 8):
+            xq = torch.from_numpy(F.synth_activations(Tq, E, seed=50 + Tq)).to(dev)
+            aqq, ascq, _ = qm.quantize_act(xq, M_stride=16)
+            lgq = torch.from_numpy(F.zipf_router_logits(Tq, NE, seed=60 + Tq)).to(dev)
+            wsq = qm.moe_workspace(Tq, NE, NU, E, Fd, device=dev)
+            xoq = torch.empty((Tq, E), device=dev)
+            msq = timed_graph(lambda i: qm.moe_grouped(ws_[0], ws_[1], ws_[2], NE, lgq, NU, aqq, ascq, xoq, wsq),
+                              args, stream)
+            ebytes = Tq * NU * 3 * F.weight_bytes(F.IQ4_XS, Fd, E)  # (upper bound: distinct experts x 3 matrices)
+            dec[str(Tq)] = {"us_per_call": round(msq * 1e3, 1), "expert_bytes_upper_bound": ebytes}
+        out["moe"]["decode"] = dec
         for w_ in ws_:
             w_.release()
 

@@ -136,7 +136,7 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
 
 /* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). */
 typedef struct {
-  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, total;
+  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, hf, total;
   int slots, max_tiles, tile_rows;
 } qm_moe_ws_layout;
 int qmatmul_moe_ws_layout(int T, int NE, int NU, int E, int F, qm_moe_ws_layout* out);

@@ -58,6 +58,8 @@ def test_moe_grouped_matches_oracle(qm, dev, qtype, NE, E, Fd, T, NU):
     ref = oracle.moe_forward(qtype, s["Wg"], qtype, s["Wu"], qtype, s["Wd"], NE, E, Fd, s["lg"], NU,
                              s["aq"].cpu().numpy(), s["asc"].cpu().numpy())
     assert rel_err(s["out"].cpu().numpy(), ref) < 1e-4
+    if T * NU <= 64:
+        return  # (decode sizes take the GEMV-shaped kernels: no slot permutation is built)
     # the device permutation: slots of each expert contiguous, a bijection onto (token, k)
     L = qm.moe_ws_layout(T, NE, NU, E, Fd)
     ws = s["ws"].cpu().numpy()
@@ -106,3 +108,24 @@ def test_moe_baseline_config_token_sample(qm, dev):
     ref = oracle.moe_forward(F.IQ4_XS, s["Wg"], F.IQ4_XS, s["Wu"], F.IQ4_XS, s["Wd"], NE, E, Fd, s["lg"][pick], NU,
                              aq, asc)
     assert rel_err(s["out"].cpu().numpy()[pick], ref) < 1e-4
+
+
+@pytest.mark.parametrize("qtype,NE,E,Fd,T,NU", [(F.IQ4_XS, 256, 2048, 512, 1, 8), (F.IQ4_XS, 256, 2048, 512, 8, 8),
+                                                (F.IQ3_S, 16, 1024, 1024, 3, 4), (F.Q8_0, 8, 512, 2048, 2, 2)])
+def test_moe_decode_sizes_match_oracle(qm, dev, qtype, NE, E, Fd, T, NU):
+    """T * NU <= 64: the GEMV-shaped decode kernels (gate/up -> h -> down + combine in k order)."""
+    import torch
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, qtype, seed=7 * T + NU)
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    torch.cuda.synchronize()
+    ref = oracle.moe_forward(qtype, s["Wg"], qtype, s["Wu"], qtype, s["Wd"], NE, E, Fd, s["lg"], NU,
+                             s["aq"].cpu().numpy(), s["asc"].cpu().numpy())
+    assert rel_err(s["out"].cpu().numpy(), ref) < 1e-4
+    first = s["out"].clone()
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    torch.cuda.synchronize()
+    assert torch.equal(s["out"], first)
+    base = torch.full_like(first, -0.25)
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], base, s["ws"], accumulate=1)
+    torch.cuda.synchronize()
+    assert torch.equal(base, -0.25 + first)
