@@ -11,6 +11,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqmatmul.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HOST_SOURCES = ["qm_gguf.cpp"]  # host-only C++ (g++)
 SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemm.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
@@ -18,6 +19,15 @@ FLAGS = [
     # packed FP32 instructions stay off: every f32 op is a plain VALU op
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+
+
+def _compile_host(src):
+    obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on {src}:\n{r.stderr}")
+    return obj
 
 
 def _compile(src):
@@ -36,7 +46,7 @@ def _compile(src):
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(_compile, SOURCES)) + list(ex.map(_compile_host, HOST_SOURCES))
     tmp = LIB + ".tmp"
     r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs],
                        capture_output=True, text=True)

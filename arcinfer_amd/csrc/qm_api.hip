@@ -8,6 +8,7 @@
 #include <mutex>
 
 #include "../../include/qmatmul.h"
+#include "qm_gguf.h"
 #include "qm_launch.h"
 
 struct qm_weight {
@@ -488,6 +489,95 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   }
   if (e == hipSuccess) e = qm::launch_moe_combine(x, y, inv, T, NU, E, accumulate, s);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
+}
+
+
+// ---- GGUF files ----------------------------------------------------------------------------------------------------
+struct qm_gguf {
+  std::unique_ptr<qm::Gguf> g;
+};
+
+int qmatmul_gguf_open(const char* path, qm_gguf** out) {
+  if (!path || !out) return fail(QM_ERR_ARG, "qmatmul_gguf_open: null pointer");
+  *out = nullptr;
+  std::string err;
+  std::unique_ptr<qm::Gguf> g = qm::Gguf::open(path, err);
+  if (!g) return fail(QM_ERR_ARG, "qmatmul_gguf_open: %s: %s", path, err.c_str());
+  *out = new qm_gguf{std::move(g)};
+  return QM_OK;
+}
+
+int qmatmul_gguf_close(qm_gguf* g) {
+  delete g;
+  return QM_OK;
+}
+
+int qmatmul_gguf_tensor_count(const qm_gguf* g, int* n) {
+  if (!g || !n) return fail(QM_ERR_ARG, "qmatmul_gguf_tensor_count: null pointer");
+  *n = (int)g->g->tensors.size();
+  return QM_OK;
+}
+
+int qmatmul_gguf_find_tensor(const qm_gguf* g, const char* name, int* index) {
+  if (!g || !name || !index) return fail(QM_ERR_ARG, "qmatmul_gguf_find_tensor: null pointer");
+  auto it = g->g->index.find(name);
+  if (it == g->g->index.end()) return fail(QM_ERR_ARG, "qmatmul_gguf_find_tensor: no tensor %s", name);
+  *index = (int)it->second;
+  return QM_OK;
+}
+
+int qmatmul_gguf_tensor_info(const qm_gguf* g, int i, const char** name, int* type, int* n_dims, uint64_t* dims,
+                             const void** data, uint64_t* nbytes) {
+  if (!g) return fail(QM_ERR_ARG, "qmatmul_gguf_tensor_info: null handle");
+  if (i < 0 || i >= (int)g->g->tensors.size()) return fail(QM_ERR_ARG, "qmatmul_gguf_tensor_info: index %d", i);
+  const qm::GgufTensorInfo& t = g->g->tensors[i];
+  if (name) *name = t.name.c_str();
+  if (type) *type = (int)t.type;
+  if (n_dims) *n_dims = (int)t.n_dims;
+  if (dims)
+    for (int d = 0; d < 8; ++d) dims[d] = d < (int)t.n_dims ? t.dims[d] : 0;
+  if (data) *data = t.data;
+  if (nbytes) *nbytes = t.nbytes;
+  return QM_OK;
+}
+
+static const qm::GgufValue* gguf_value(const qm_gguf* g, const char* key, const char* fn) {
+  if (!g || !key) {
+    fail(QM_ERR_ARG, "%s: null pointer", fn);
+    return nullptr;
+  }
+  auto it = g->g->kv.find(key);
+  if (it == g->g->kv.end()) {
+    fail(QM_ERR_ARG, "%s: no key %s", fn, key);
+    return nullptr;
+  }
+  return &it->second;
+}
+
+int qmatmul_gguf_get_int(const qm_gguf* g, const char* key, int64_t* out) {
+  const qm::GgufValue* v = gguf_value(g, key, "qmatmul_gguf_get_int");
+  if (!v) return QM_ERR_ARG;
+  if (v->type == qm::GV_STR || v->type == qm::GV_ARR)
+    return fail(QM_ERR_TYPE, "qmatmul_gguf_get_int: %s is not a number", key);
+  if (out) *out = v->i;
+  return QM_OK;
+}
+
+int qmatmul_gguf_get_float(const qm_gguf* g, const char* key, double* out) {
+  const qm::GgufValue* v = gguf_value(g, key, "qmatmul_gguf_get_float");
+  if (!v) return QM_ERR_ARG;
+  if (v->type == qm::GV_STR || v->type == qm::GV_ARR)
+    return fail(QM_ERR_TYPE, "qmatmul_gguf_get_float: %s is not a number", key);
+  if (out) *out = v->f;
+  return QM_OK;
+}
+
+int qmatmul_gguf_get_str(const qm_gguf* g, const char* key, const char** out) {
+  const qm::GgufValue* v = gguf_value(g, key, "qmatmul_gguf_get_str");
+  if (!v) return QM_ERR_ARG;
+  if (v->type != qm::GV_STR) return fail(QM_ERR_TYPE, "qmatmul_gguf_get_str: %s is not a string", key);
+  if (out) *out = v->s.c_str();
+  return QM_OK;
 }
 
 }  // extern "C"

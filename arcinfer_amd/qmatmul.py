@@ -38,6 +38,15 @@ SIGNATURES = [
     ("qmatmul_rmsnorm_quant", _I, [_P, _I, _P, _I, _I, _I, _c.c_float, _P, _P, _P, _P, _I, _P]),
     ("qmatmul_swiglu_quant", _I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_add_norm_quant", _I, [_P, _P, _P, _I, _c.c_float, _c.c_float, _P, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_gguf_open", _I, [_c.c_char_p, _c.POINTER(_P)]),
+    ("qmatmul_gguf_close", _I, [_P]),
+    ("qmatmul_gguf_tensor_count", _I, [_P, _c.POINTER(_I)]),
+    ("qmatmul_gguf_find_tensor", _I, [_P, _c.c_char_p, _c.POINTER(_I)]),
+    ("qmatmul_gguf_tensor_info", _I, [_P, _I, _c.POINTER(_c.c_char_p), _c.POINTER(_I), _c.POINTER(_I),
+                                      _c.POINTER(_c.c_uint64), _c.POINTER(_P), _c.POINTER(_c.c_uint64)]),
+    ("qmatmul_gguf_get_int", _I, [_P, _c.c_char_p, _c.POINTER(_c.c_int64)]),
+    ("qmatmul_gguf_get_float", _I, [_P, _c.c_char_p, _c.POINTER(_c.c_double)]),
+    ("qmatmul_gguf_get_str", _I, [_P, _c.c_char_p, _c.POINTER(_c.c_char_p)]),
 ]
 
 
@@ -253,3 +262,77 @@ def add_norm_quant(x, t, w, eps, s, w2=None, M_stride=None, stream=None):
     _call("qmatmul_add_norm_quant", _ptr(x), _ptr(t), _ptr(w), K, float(eps), float(s), _ptr(w2), M, Ms, _ptr(aq),
           _ptr(asc), _ptr(absum), _stream(stream))
     return aq, asc, absum
+
+
+class GgufTensor:
+    def __init__(self, name, qtype, dims, data, nbytes):
+        self.name, self.qtype, self.dims, self.data, self.nbytes = name, qtype, dims, data, nbytes
+
+    @property
+    def K(self):
+        return self.dims[0]
+
+    @property
+    def rows(self):
+        r = 1
+        for d in self.dims[1:]:
+            r *= d
+        return r
+
+    def numpy(self):
+        """The tensor's bytes as a uint8 numpy view of the mapping (valid while the file is open)."""
+        import numpy as np
+        return np.ctypeslib.as_array((ctypes.c_uint8 * self.nbytes).from_address(self.data))
+
+
+class GgufFile:
+    """A mapped GGUF file (qmatmul_gguf_*): tensors by name, metadata by key."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _call("qmatmul_gguf_open", os.fsencode(path), ctypes.byref(h))
+        self.handle = h
+
+    def __len__(self):
+        n = ctypes.c_int()
+        _call("qmatmul_gguf_tensor_count", self.handle, ctypes.byref(n))
+        return n.value
+
+    def tensor(self, key):
+        i = key
+        if isinstance(key, str):
+            idx = ctypes.c_int()
+            _call("qmatmul_gguf_find_tensor", self.handle, key.encode(), ctypes.byref(idx))
+            i = idx.value
+        name, t, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+        dims = (ctypes.c_uint64 * 8)()
+        data, nb = ctypes.c_void_p(), ctypes.c_uint64()
+        _call("qmatmul_gguf_tensor_info", self.handle, i, ctypes.byref(name), ctypes.byref(t), ctypes.byref(nd), dims,
+              ctypes.byref(data), ctypes.byref(nb))
+        return GgufTensor(name.value.decode(), t.value, [int(d) for d in dims[:nd.value]], data.value or 0, nb.value)
+
+    def get_int(self, key):
+        v = ctypes.c_int64()
+        _call("qmatmul_gguf_get_int", self.handle, key.encode(), ctypes.byref(v))
+        return v.value
+
+    def get_float(self, key):
+        v = ctypes.c_double()
+        _call("qmatmul_gguf_get_float", self.handle, key.encode(), ctypes.byref(v))
+        return v.value
+
+    def get_str(self, key):
+        v = ctypes.c_char_p()
+        _call("qmatmul_gguf_get_str", self.handle, key.encode(), ctypes.byref(v))
+        return v.value.decode()
+
+    def close(self):
+        if self.handle:
+            _call("qmatmul_gguf_close", self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()

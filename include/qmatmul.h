@@ -150,6 +150,23 @@ int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* 
                            int32_t* isum, int32_t* msum, void* stream);
 int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream);
 
+/* GGUF files (host side). Maps a GGUF v2/v3 file read-only and indexes its metadata and tensors, so a weight can
+ * go to qmatmul_prepare_weight straight from the mapping (raw_on_device = 0; rows = dims[1] * dims[2] * ..., K =
+ * dims[0]). Replaces the reference's GgufFile (src/gguf.h:85-305; Win32 mapping there, POSIX here; split-model parts
+ * are not followed). Pointers returned by the accessors live until qmatmul_gguf_close. Reading is bounds-checked:
+ * truncated or malformed files fail with QM_ERR_ARG and a message. Metadata: numbers of any GGUF numeric type read
+ * through get_int / get_float; strings through get_str; arrays are indexed but not exposed. */
+typedef struct qm_gguf qm_gguf;
+int qmatmul_gguf_open(const char* path, qm_gguf** out);
+int qmatmul_gguf_close(qm_gguf* g);
+int qmatmul_gguf_tensor_count(const qm_gguf* g, int* n);
+int qmatmul_gguf_find_tensor(const qm_gguf* g, const char* name, int* index);
+int qmatmul_gguf_tensor_info(const qm_gguf* g, int i, const char** name, int* type, int* n_dims, uint64_t* dims,
+                             const void** data, uint64_t* nbytes);
+int qmatmul_gguf_get_int(const qm_gguf* g, const char* key, int64_t* out);
+int qmatmul_gguf_get_float(const qm_gguf* g, const char* key, double* out);
+int qmatmul_gguf_get_str(const qm_gguf* g, const char* key, const char** out);
+
 #ifdef __cplusplus
 }
 #endif
