@@ -27,6 +27,13 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
     r.q0 = ld_stream16(qp);
     r.q1 = ld_stream16(qp + 16);
     r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (TYPE == T_Q6_K) {
+    r.q0 = ld_stream16(qp);
+    const uint32_t* q = (const uint32_t*)(qp + 16);
+    r.q1.x = __builtin_nontemporal_load(q);
+    r.q1.y = __builtin_nontemporal_load(q + 1);
+    r.h.x = ((const uint16_t*)hp)[b & 7];  // the block's two int8 scales
+    r.h.y = ((const uint16_t*)hp)[8];      // f16 d
   } else if constexpr (TYPE == T_IQ3_S) {
     const uint32_t* q = (const uint32_t*)qp;
     r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2),
@@ -52,13 +59,29 @@ __device__ __forceinline__ RawBlk load_block(const WView& w, int n, int b) {
 }
 
 // Decodes a loaded 32-block (index ib = b % 8 in its superblock): w[k] = elements 4k..4k+3 (int8x4), the integer
-// scale sc (and min mn), the float scale d (and dmin).
+// scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K), the min mn, the float scales d (and dmin). Q6_K's
+// values come out as the stored 6-bit numbers 0..63 (the offset of 32 is removed by block_product).
 template <int TYPE>
 __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int ib,
-                                               const KvTab& kv, uint32_t wd[8], int& sc, int& mn, float& d,
-                                               float& dmin) {
+                                               const KvTab& kv, uint32_t wd[8], int& sc, int& sc1, int& mn,
+                                               float& d, float& dmin) {
   mn = 0;
   dmin = 0.0f;
+  if constexpr (TYPE == T_Q6_K) {
+    const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
+    const uint32_t A = r.q1.x, B = r.q1.y;  // high 2 bits of elements 0-15 / 16-31: byte i, bits 2k = element 4k+i
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ha = k < 2 ? A << (4 - 2 * k) : A >> (2 * k - 4);
+      const uint32_t hb = k < 2 ? B << (4 - 2 * k) : B >> (2 * k - 4);
+      wd[k] = (qq[k] & 0x0F0F0F0Fu) | (ha & 0x30303030u);
+      wd[4 + k] = ((qq[k] >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u);
+    }
+    sc = (int)(int8_t)(r.h.x & 0xFFu);
+    sc1 = (int)(int8_t)((r.h.x >> 8) & 0xFFu);
+    d = h2f(r.h.y);
+    return;
+  }
   if constexpr (TYPE == T_Q8_0) {
     wd[0] = r.q0.x; wd[1] = r.q0.y; wd[2] = r.q0.z; wd[3] = r.q0.w;
     wd[4] = r.q1.x; wd[5] = r.q1.y; wd[6] = r.q1.z; wd[7] = r.q1.w;
@@ -83,7 +106,7 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     }
     d = h2f(r.h.x);
     sc = iq4xs_scale(r.h.x, r.h.y, ib);
-  } else {  // IQ3_S
+  } else if constexpr (TYPE == T_IQ3_S) {
     const uint32_t qh = ((ib < 4 ? r.h.x : r.h.y) >> (8 * (ib & 3))) & 0xFFu;
     iq3s_pair<0>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[0], wd[1]);
     iq3s_pair<1>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[2], wd[3]);
@@ -92,6 +115,58 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     sc = 1 + 2 * (int)((r.h.z >> (4 * ib)) & 0xFu);
     d = h2f(r.h.w);
   }
+  sc1 = sc;
+}
+
+// One 32-block's integer products with one token's int8 activations (x0: elements 0-15, x1: 16-31; bs0 / bs1 their
+// per-16 sums, used by Q4_K and Q6_K): iv = sc0 * lo + sc1 * hi over the signed quants and, for Q4_K, the min term
+// mv = mn * (bs0 + bs1) -- the reference's per-block integers (zero/kernels/decode.cl:695-706). Q6_K's stored
+// values q carry an offset of 32: sum a * (q - 32) = lo - 32 * bs.
+struct BlockInts {
+  int iv, mv;
+  float d, dmin;
+};
+
+// iv / mv of decoded words wd with one token (see BlockInts); d / dmin are left to the caller
+template <int TYPE>
+__device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1, int mn, const uint4& x0,
+                                          const uint4& x1, int bs0, int bs1, int& iv, int& mv) {
+  int lo = dot4(x0.x, wd[0], 0);
+  lo = dot4(x0.y, wd[1], lo);
+  lo = dot4(x0.z, wd[2], lo);
+  lo = dot4(x0.w, wd[3], lo);
+  int hi = dot4(x1.x, wd[4], 0);
+  hi = dot4(x1.y, wd[5], hi);
+  hi = dot4(x1.z, wd[6], hi);
+  hi = dot4(x1.w, wd[7], hi);
+  if constexpr (Traits<TYPE>::SC16) {
+    // (|lo - 32 bs| < 2^17 and |sc| < 2^7: the 24-bit multiplies are exact)
+    iv = __mul24(sc, lo - 32 * bs0) + __mul24(sc1, hi - 32 * bs1);
+  } else if constexpr (TYPE == T_Q8_0) {
+    iv = lo + hi;
+  } else {
+    iv = __mul24(sc, lo + hi);
+  }
+  mv = Traits<TYPE>::MINS ? __mul24(mn, bs0 + bs1) : 0;
+}
+
+template <int TYPE>
+__device__ __forceinline__ BlockInts block_product(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int ib,
+                                                   const KvTab& kv, const uint4& x0, const uint4& x1, int bs0,
+                                                   int bs1) {
+  uint32_t wd[8];
+  int sc, sc1, mn;
+  BlockInts o;
+  decode_block32<TYPE>(r, lds, ib, kv, wd, sc, sc1, mn, o.d, o.dmin);
+  block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, bs0, bs1, o.iv, o.mv);
+  return o;
+}
+
+// the reference's per-block float term: sa * d * (float)iv [ - sa * dmin * (float)mv ] (decode.cl:702-706)
+template <int TYPE>
+__device__ __forceinline__ float block_value(float sa, const BlockInts& b) {
+  if constexpr (Traits<TYPE>::MINS) return sa * (b.d * (float)b.iv - b.dmin * (float)b.mv);
+  else return sa * b.d * (float)b.iv;
 }
 
 }  // namespace qm

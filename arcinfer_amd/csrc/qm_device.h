@@ -9,6 +9,9 @@
 //   Q4_K   QB 16: byte t = q[t] | q[16+t] << 4       HB 16: f16 d, f16 dmin, 12 bytes of 6-bit scales/mins (GGUF)
 //   IQ4_XS QB 16: byte t = i[t] | i[16+t] << 4       HB  8: f16 d, u16 scales_h, u8 scales_l[4] (GGUF)
 //   IQ3_S  QB 12: 8 index low bytes, 4 sign bytes    HB 16: qh[8], scales[4], f16 d, 2 bytes zero
+//   Q6_K   QB 24: byte t = low4[t] | low4[16+t] << 4, then two words of 2-bit high parts: word h (h = 0, 1),
+//                 byte i, bits 2k..2k+1 = high2[16h + 4k + i]          HB 20: int8 scales[16] (per 16), f16 d, 2 zero
+// (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
 // (Q4_K's GGUF nibble order -- 64-element chunks, low nibbles first -- is regrouped to IQ4_XS's per-32 order, so
 // the 4-bit types share one unpacking path.)
 #pragma once
@@ -20,13 +23,18 @@
 
 namespace qm {
 
-enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_IQ3_S = 21, T_IQ4_XS = 23 };
+enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_IQ3_S = 21, T_IQ4_XS = 23 };
 
 template <int TYPE> struct Traits;
-template <> struct Traits<T_Q8_0> { static constexpr int QB = 32, HB = 16, GGUF_SB = 272; static constexpr bool MINS = false; };
-template <> struct Traits<T_Q4_K> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = true; };
-template <> struct Traits<T_IQ4_XS> { static constexpr int QB = 16, HB = 8, GGUF_SB = 136; static constexpr bool MINS = false; };
-template <> struct Traits<T_IQ3_S> { static constexpr int QB = 12, HB = 16, GGUF_SB = 110; static constexpr bool MINS = false; };
+// MINS: per-block mins (the activation block sums enter the result); SC16: two integer scales per 32-block (one per
+// 16) and quants stored with an offset of 32 (removed with the per-16 activation sums)
+template <> struct Traits<T_Q8_0> { static constexpr int QB = 32, HB = 16, GGUF_SB = 272; static constexpr bool MINS = false, SC16 = false; };
+template <> struct Traits<T_Q4_K> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = true, SC16 = false; };
+template <> struct Traits<T_Q6_K> { static constexpr int QB = 24, HB = 20, GGUF_SB = 210; static constexpr bool MINS = false, SC16 = true; };
+template <> struct Traits<T_IQ4_XS> { static constexpr int QB = 16, HB = 8, GGUF_SB = 136; static constexpr bool MINS = false, SC16 = false; };
+template <> struct Traits<T_IQ3_S> { static constexpr int QB = 12, HB = 16, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false; };
+// whether the kernels need the per-16 activation sums (absum)
+template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
 
 // A prepared weight as the kernels see it.
 struct WView {

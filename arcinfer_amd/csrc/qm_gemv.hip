@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     RawBlk raw[U][R];
     uint32_t av[U][TB][8];
     float sa[U][TB];
-    int bs[U][TB];
+    int bs0[U][TB], bs1[U][TB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int b = min(b0 + LPR * u, nb - 1);  // (past the row's end: reload its last block, masked below)
@@ -53,10 +53,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         av[u][t][0] = x0.x; av[u][t][1] = x0.y; av[u][t][2] = x0.z; av[u][t][3] = x0.w;
         av[u][t][4] = x1.x; av[u][t][5] = x1.y; av[u][t][6] = x1.z; av[u][t][7] = x1.w;
         sa[u][t] = DUMP ? 0.0f : a.asc[(size_t)b * a.M_stride + tt];
-        if constexpr (Traits<TYPE>::MINS)
-          bs[u][t] = (int)a.absum[(size_t)(2 * b) * a.M_stride + tt] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
-        else
-          bs[u][t] = 0;
+        if constexpr (kNeedsBsum<TYPE>) {
+          bs0[u][t] = a.absum[(size_t)(2 * b) * a.M_stride + tt];
+          bs1[u][t] = a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
+        } else {
+          bs0[u][t] = bs1[u][t] = 0;
+        }
       }
     }
 #pragma unroll
@@ -66,26 +68,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         uint32_t wd[8];
-        int sc, mn;
-        float d, dmin;
-        decode_block32<TYPE>(raw[u][r], &lds, b & 7, kv, wd, sc, mn, d, dmin);
+        int sc, sc1, mn;
+        BlockInts bi;
+        decode_block32<TYPE>(raw[u][r], &lds, b & 7, kv, wd, sc, sc1, mn, bi.d, bi.dmin);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
-          int isum = 0;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) isum = dot4(av[u][t][k], wd[k], isum);
-          const int iv = sc * isum;
+          const uint4 x0 = make_uint4(av[u][t][0], av[u][t][1], av[u][t][2], av[u][t][3]);
+          const uint4 x1 = make_uint4(av[u][t][4], av[u][t][5], av[u][t][6], av[u][t][7]);
+          block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, bs0[u][t], bs1[u][t], bi.iv, bi.mv);
           if constexpr (DUMP) {
             if (live && t < T && row0 + r < rows) {
               const size_t o = ((size_t)t * rows + (row0 + r)) * nb + b;
-              a.dbg_isum[o] = iv;
-              if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = mn * bs[u][t];
+              a.dbg_isum[o] = bi.iv;
+              if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = bi.mv;
             }
           } else if (live) {
-            if constexpr (Traits<TYPE>::MINS)
-              acc[r][t] += sa[u][t] * (d * (float)iv - dmin * (float)(mn * bs[u][t]));
-            else
-              acc[r][t] += sa[u][t] * d * (float)iv;
+            acc[r][t] += block_value<TYPE>(sa[u][t], bi);
           }
         }
       }
@@ -120,7 +118,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
   const int K = a.w.K, nb = K / 32, rows = a.w.rows;
   uint8_t* sq = (uint8_t*)smem;            // [2][nb][16] int8 planes
   float* ssc = (float*)(sq + (size_t)K);    // [nb] scales
-  int* sbs = (int*)(ssc + nb);              // [nb] per-32 sums (Q4_K)
+  int* sbs = (int*)(ssc + nb);              // [nb] per-16 sums of each block, packed int16 pairs (Q4_K, Q6_K)
   const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
   const int nch = (nb / 32 + CH - 1) / CH;  // steps per row
   const int row_base = blockIdx.x * 8 * rpg + grp;
@@ -149,7 +147,8 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
   }
   for (int b = threadIdx.x; b < nb; b += 256) {
     ssc[b] = a.asc[(size_t)b * a.M_stride];
-    if constexpr (Traits<TYPE>::MINS) sbs[b] = (int)a.absum[(size_t)(2 * b) * a.M_stride] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride];
+    if constexpr (kNeedsBsum<TYPE>)
+      sbs[b] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride] | ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride] << 16);
   }
   __syncthreads();
 
@@ -162,25 +161,10 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
     for (int u = 0; u < CH; ++u) {
       const int b = gl + 32 * (c * CH + u);
       if (EXACT || b < nb) {
-        uint32_t wd[8];
-        int sc, mn;
-        float d, dmin;
-        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, mn, d, dmin);
         const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
-        int isum = dot4(x0.x, wd[0], 0);
-        isum = dot4(x0.y, wd[1], isum);
-        isum = dot4(x0.z, wd[2], isum);
-        isum = dot4(x0.w, wd[3], isum);
-        isum = dot4(x1.x, wd[4], isum);
-        isum = dot4(x1.y, wd[5], isum);
-        isum = dot4(x1.z, wd[6], isum);
-        isum = dot4(x1.w, wd[7], isum);
-        const int iv = __mul24(sc, isum);
-        const float sa = ssc[b];
-        if constexpr (Traits<TYPE>::MINS)
-          acc += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[b]));
-        else
-          acc += sa * d * (float)iv;
+        const int bp = kNeedsBsum<TYPE> ? sbs[b] : 0;
+        const BlockInts bi = block_product<TYPE>(cur[u], &lds, b & 7, kv, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16);
+        acc += block_value<TYPE>(ssc[b], bi);
       }
     }
     if (c == nch - 1) {
@@ -244,8 +228,9 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   for (int i = threadIdx.x; i < nb * TB; i += 256) {
     const int t = i / nb, b = i % nb, tt = min(t, T - 1);
     ssc[i] = a.asc[(size_t)b * a.M_stride + tt];
-    if constexpr (Tr::MINS)
-      sbs[i] = (int)a.absum[(size_t)(2 * b) * a.M_stride + tt] + (int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
+    if constexpr (kNeedsBsum<TYPE>)
+      sbs[i] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride + tt] |
+               ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt] << 16);
   }
   __syncthreads();
   const KvTab kv = kv_tab();
@@ -258,27 +243,16 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
       const int b = gl + LPR * u;
       if (EXACT || b < nb) {
         uint32_t wd[8];
-        int sc, mn;
-        float d, dmin;
-        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, mn, d, dmin);
+        int sc, sc1, mn;
+        BlockInts bi;
+        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, sc1, mn, bi.d, bi.dmin);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
           const uint8_t* st = sq + (size_t)t * K;
           const uint4 x0 = *(const uint4*)(st + b * 16), x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
-          int isum = dot4(x0.x, wd[0], 0);
-          isum = dot4(x0.y, wd[1], isum);
-          isum = dot4(x0.z, wd[2], isum);
-          isum = dot4(x0.w, wd[3], isum);
-          isum = dot4(x1.x, wd[4], isum);
-          isum = dot4(x1.y, wd[5], isum);
-          isum = dot4(x1.z, wd[6], isum);
-          isum = dot4(x1.w, wd[7], isum);
-          const int iv = __mul24(sc, isum);
-          const float sa = ssc[t * nb + b];
-          if constexpr (Tr::MINS)
-            acc[t] += sa * (d * (float)iv - dmin * (float)__mul24(mn, sbs[t * nb + b]));
-          else
-            acc[t] += sa * d * (float)iv;
+          const int bp = kNeedsBsum<TYPE> ? sbs[t * nb + b] : 0;
+          block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16, bi.iv, bi.mv);
+          acc[t] += block_value<TYPE>(ssc[t * nb + b], bi);
         }
       }
     }
@@ -316,7 +290,7 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
 // LDS bytes of gemvs_kernel for TB tokens
 static size_t gemvs_lds(int type, int K, int TB) {
   const int nb = K / 32;
-  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K ? sizeof(int) * nb : 0));
+  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q6_K ? sizeof(int) * nb : 0));
 }
 
 template <int TYPE, int LPR, int CH, bool EXACT, int TB>
@@ -346,7 +320,7 @@ static hipError_t go1(const GemvArgs& a, hipStream_t s) {
   int rpg = 1;
   while (rpg < 16 && (rows + 8 * rpg * 2 - 1) / (8 * rpg * 2) >= 1024) rpg *= 2;
   const unsigned grid = (unsigned)((rows + 8 * rpg - 1) / (8 * rpg));
-  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (Traits<TYPE>::MINS ? sizeof(int) * nb : 0);
+  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (kNeedsBsum<TYPE> ? sizeof(int) * nb : 0);
   gemv1_kernel<TYPE, CH, EXACT><<<grid, 256, shm, s>>>(a, rpg);
   return hipGetLastError();
 }
@@ -434,6 +408,7 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_Q4_K: return dispatch<T_Q4_K>(a, s);
     case T_IQ4_XS: return dispatch<T_IQ4_XS>(a, s);
     case T_IQ3_S: return dispatch<T_IQ3_S>(a, s);
+    case T_Q6_K: return dispatch<T_Q6_K>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

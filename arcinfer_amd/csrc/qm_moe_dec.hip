@@ -11,20 +11,10 @@ namespace {
 template <int TYPE>
 __device__ __forceinline__ int block_isum(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int b,
                                           const KvTab& kv, const uint8_t* sq, int nb, float& d) {
-  uint32_t wd[8];
-  int sc, mn;
-  float dmin;
-  decode_block32<TYPE>(r, lds, b & 7, kv, wd, sc, mn, d, dmin);
   const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
-  int isum = dot4(x0.x, wd[0], 0);
-  isum = dot4(x0.y, wd[1], isum);
-  isum = dot4(x0.z, wd[2], isum);
-  isum = dot4(x0.w, wd[3], isum);
-  isum = dot4(x1.x, wd[4], isum);
-  isum = dot4(x1.y, wd[5], isum);
-  isum = dot4(x1.z, wd[6], isum);
-  isum = dot4(x1.w, wd[7], isum);
-  return __mul24(sc, isum);
+  const BlockInts bi = block_product<TYPE>(r, lds, b & 7, kv, x0, x1, 0, 0);  // (types without per-16 sums)
+  d = bi.d;
+  return bi.iv;
 }
 
 }  // namespace

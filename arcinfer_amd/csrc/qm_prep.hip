@@ -41,6 +41,31 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     // d, scales_h, scales_l[4] | qs[128] (block ib = qs[16 ib .. 16 ib + 15], already per-32)
     for (int e = 0; e < 8; ++e) h[e] = p[e];
     for (int e = 0; e < 128; ++e) q[e] = p[8 + e];
+  } else if constexpr (TYPE == T_Q6_K) {
+    // ql[128] | qh[64] | scales[16] | d (src/quants.h:125-141): element 128n + 32c + l has its low 4 bits in
+    // ql[64n + l + 32 (c & 1)] (nibble c >> 1) and its high 2 bits in qh[32n + l] (bits 2c..2c+1); block b = 4n + c
+    const uint8_t *ql = p, *qh = p + 128;
+    for (int b = 0; b < 8; ++b) {
+      const int n2 = b >> 2, c = b & 3;
+      uint8_t lo4[32], hi2[32];
+      for (int l = 0; l < 32; ++l) {
+        lo4[l] = (uint8_t)((ql[64 * n2 + l + 32 * (c & 1)] >> (4 * (c >> 1))) & 0xF);
+        hi2[l] = (uint8_t)((qh[32 * n2 + l] >> (2 * c)) & 3);
+      }
+      uint8_t* dst = q + 24 * b;
+      for (int t = 0; t < 16; ++t) dst[t] = (uint8_t)(lo4[t] | (lo4[16 + t] << 4));
+      for (int hw = 0; hw < 2; ++hw)
+        for (int i = 0; i < 4; ++i) {
+          uint8_t v = 0;
+          for (int k = 0; k < 4; ++k) v |= (uint8_t)(hi2[16 * hw + 4 * k + i] << (2 * k));
+          dst[16 + 4 * hw + i] = v;
+        }
+    }
+    for (int e = 0; e < 16; ++e) h[e] = p[192 + e];
+    h[16] = p[208];
+    h[17] = p[209];
+    h[18] = 0;
+    h[19] = 0;
   } else {  // IQ3_S: d | qs[64] | qh[8] | signs[32] | scales[4]
     for (int b = 0; b < 8; ++b) {
       for (int e = 0; e < 8; ++e) q[12 * b + e] = p[2 + 8 * b + e];
@@ -63,6 +88,7 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t*
     case T_Q4_K: repack_kernel<T_Q4_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

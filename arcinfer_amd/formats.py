@@ -1,17 +1,17 @@
-"""GGUF block geometry of the four weight types of the path, and seeded synthetic weights in GGUF block form.
+"""GGUF block geometry of the weight types of the path, and seeded synthetic weights in GGUF block form.
 
-Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_K 256 / 144, IQ3_S 256 / 110,
-IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
+Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_K 256 / 144, Q6_K 256 / 210,
+IQ3_S 256 / 110, IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
 bytes: every quant / index / sign / sub-scale bit uniform, the f16 super-scales |N(0, sigma)|.
 """
 import numpy as np
 
-Q8_0, Q4_K, IQ3_S, IQ4_XS = 8, 12, 21, 23
-TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
+Q8_0, Q4_K, Q6_K, IQ3_S, IQ4_XS = 8, 12, 14, 21, 23
+TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 # bytes of one 256-element superblock (Q8_0: 8 blocks of 34)
-SB_BYTES = {Q8_0: 272, Q4_K: 144, IQ3_S: 110, IQ4_XS: 136}
+SB_BYTES = {Q8_0: 272, Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
 
 
 def row_bytes(qtype, K):
@@ -37,6 +37,7 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     Q4_K:   quants, 6-bit scales and mins uniform (all bits random), d and dmin = f16(|N(0, 0.01)|)
     IQ4_XS: nibbles and 6-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
     IQ3_S:  9-bit grid indices, signs and 4-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
+    Q6_K:   6-bit quants and int8 per-16 scales uniform, d = f16(|N(0, 0.01)|) (d is the last field)
     """
     rng = np.random.default_rng(seed)
     nsb = K // 256
@@ -53,8 +54,9 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     sb = SB_BYTES[qtype]
     raw = rng.integers(0, 256, size=(N * nsb, sb), dtype=np.uint8)
     d = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
-    raw[:, 0] = d & 0xFF
-    raw[:, 1] = d >> 8
+    at = 208 if qtype == Q6_K else 0
+    raw[:, at] = d & 0xFF
+    raw[:, at + 1] = d >> 8
     if qtype == Q4_K:
         dm = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
         raw[:, 2] = dm & 0xFF

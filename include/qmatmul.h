@@ -29,7 +29,7 @@ extern "C" {
 #endif
 
 /* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
-typedef enum { QM_Q8_0 = 8, QM_Q4_K = 12, QM_IQ3_S = 21, QM_IQ4_XS = 23 } qm_type;
+typedef enum { QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q6_K = 14, QM_IQ3_S = 21, QM_IQ4_XS = 23 } qm_type;
 
 typedef enum {
   QM_OK = 0,
@@ -54,7 +54,8 @@ const char* qmatmul_last_error(void);
 /* Bytes of one 256-element superblock in GGUF (0 for an unsupported type); src/gguf.h:43-72. */
 size_t qmatmul_sb_bytes(int type);
 
-/* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S superblock). */
+/* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S or Q6_K
+ * superblock). */
 size_t qmatmul_weight_bytes(int type, int rows, int K);
 
 /* Prepares a weight from its GGUF bytes: rows x (K/256) superblocks, row-major, as stored in a GGUF tensor (a
@@ -100,7 +101,7 @@ int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, floa
 
 /* Decode GEMV, T tokens (1..8) against one read of the weight:
  *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
- * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K only.
+ * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K and Q6_K.
  * Replaces the gemv / gemv_v / gemv_mt / gemv_mt_v launches of Engine::matmul1 (zero/engine.h:3184-3232;
  * zero/kernels/decode.cl:636-737, 1074-1141, 1145-1411). */
 int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,

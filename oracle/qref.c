@@ -68,6 +68,7 @@ int qref_block_info(int type, int* blk, int* bytes) {
   switch (type) {
     case QREF_Q8_0: *blk = 32; *bytes = 34; return 0;
     case QREF_Q4_K: *blk = 256; *bytes = 144; return 0;
+    case QREF_Q6_K: *blk = 256; *bytes = 210; return 0;
     case QREF_IQ3_S: *blk = 256; *bytes = 110; return 0;
     case QREF_IQ4_XS: *blk = 256; *bytes = 136; return 0;
     default: return -1;
@@ -94,7 +95,7 @@ static void scale_min_k4(int j, const uint8_t* q, int* d, int* m) {
 }
 
 /* src/quants.h:89-315 (cases Q4_K 91-114, Q8_0 149-158, IQ3_S 240-262, IQ4_XS 297-312) */
-int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
+static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
   memset(o, 0, sizeof(*o));
   switch (type) {
     case QREF_Q4_K: {
@@ -151,8 +152,32 @@ int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
       }
       return 0;
     }
+    case QREF_Q6_K: {
+      /* src/quants.h:125-141: ql[128] | qh[64] | scales[16] (int8, per 16) | d; q = (4 low bits | 2 high bits << 4)
+       * - 32, kept signed here (the reference keeps q and subtracts 32 in dequant_value, :320) */
+      const uint8_t *ql = p, *qh = p + 128;
+      o->d = qref_fp16_to_f32(rd16(p + 208));
+      for (int i = 0; i < 16; ++i) o->sc16[i] = (int8_t)p[192 + i];
+      for (int n = 0; n < 2; ++n)
+        for (int l = 0; l < 32; ++l) {
+          const uint8_t *L = ql + 64 * n, *H = qh + 32 * n;
+          o->q[128 * n + l] = (int16_t)(((L[l] & 0xF) | (((H[l] >> 0) & 3) << 4)) - 32);
+          o->q[128 * n + l + 32] = (int16_t)(((L[l + 32] & 0xF) | (((H[l] >> 2) & 3) << 4)) - 32);
+          o->q[128 * n + l + 64] = (int16_t)(((L[l] >> 4) | (((H[l] >> 4) & 3) << 4)) - 32);
+          o->q[128 * n + l + 96] = (int16_t)(((L[l + 32] >> 4) | (((H[l] >> 6) & 3) << 4)) - 32);
+        }
+      for (int b = 0; b < 8; ++b) o->sc[b] = o->sc16[2 * b];  /* (per-32 view: the first half's scale) */
+      return 0;
+    }
     default: return -1;
   }
+}
+
+int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
+  const int r = decode_sb_raw(type, p, o);
+  if (r == 0 && type != QREF_Q6_K)
+    for (int i = 0; i < 16; ++i) o->sc16[i] = o->sc[i / 2];
+  return r;
 }
 
 /* src/quants.h:317-324 (dequant_value) via :496-555 (dequant_row): float expressions as written there */
@@ -160,6 +185,7 @@ static float dequant_value(int type, const qref_sb* o, int e) {
   switch (type) {
     case QREF_Q4_K: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - o->dmin * (float)o->mn[e / 32];
     case QREF_Q8_0: return o->d8[e / 32] * (float)o->q[e];
+    case QREF_Q6_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
     default: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - 0.0f;
   }
 }
@@ -199,7 +225,7 @@ void qref_quantize_act(const float* x, int M, int K, int M_stride, int act32, in
 /* One row's superblocks decoded once: int8 quants and per-32 integer scales / float superblock scales. */
 typedef struct {
   int8_t* q;   /* [K] */
-  int* sc;     /* [K/32] */
+  int* sc;     /* [K/16]: integer scale of each 16-element half-block */
   int* mn;     /* [K/32] */
   float* d;    /* [K/32]: d of the block's superblock (Q8_0: the block's own scale) */
   float* dmin; /* [K/32] */
@@ -211,8 +237,8 @@ static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
   for (int s = 0; s < K / 256; ++s) {
     qref_decode_sb(type, row + (size_t)s * sb, &o);
     for (int e = 0; e < 256; ++e) r->q[s * 256 + e] = (int8_t)o.q[e];
+    for (int i = 0; i < 16; ++i) r->sc[s * 16 + i] = o.sc16[i];
     for (int b = 0; b < 8; ++b) {
-      r->sc[s * 8 + b] = o.sc[b];
       r->mn[s * 8 + b] = o.mn[b];
       r->d[s * 8 + b] = type == QREF_Q8_0 ? o.d8[b] : o.d;
       r->dmin[s * 8 + b] = o.dmin;
@@ -220,16 +246,17 @@ static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
   }
 }
 
-/* decode.cl:695-706 (gemv) and 1107-1115 (gemv_v): per 32-block, int sums of int8 products; the block's value
- * sa * d * (float)(sc0 * lo + sc1 * hi) [- sa * dmin * (float)(mn0 * bs0 + mn1 * bs1) for Q4_K]; here sc0 = sc1
- * and mn0 = mn1 for all four types (scales per 32), so sc0 * lo + sc1 * hi = sc * (lo + hi). */
+/* decode.cl:695-706 (gemv) and 1107-1115 (gemv_v): per 32-block, int sums of int8 products over its two 16-element
+ * halves; the block's value sa * d * (float)(sc0 * lo + sc1 * hi) [- sa * dmin * (float)(mn0 * bs0 + mn1 * bs1) for
+ * Q4_K]; sc0 != sc1 only for Q6_K (scales per 16), mn0 = mn1 (mins per 32). */
 static double row_dot(int type, const row_dec* r, int K, const int8_t* a, const float* asc, const int16_t* absum,
                       int m, int M_stride, int32_t* bsums, int32_t* msums) {
   double acc = 0.0;
   for (int b = 0; b < K / 32; ++b) {
-    int isum = 0;
-    for (int i = 0; i < 32; ++i) isum += (int)a[32 * b + i] * (int)r->q[32 * b + i];
-    const int iv = r->sc[b] * isum;
+    int lo = 0, hi = 0;
+    for (int i = 0; i < 16; ++i) lo += (int)a[32 * b + i] * (int)r->q[32 * b + i];
+    for (int i = 16; i < 32; ++i) hi += (int)a[32 * b + i] * (int)r->q[32 * b + i];
+    const int iv = r->sc[2 * b] * lo + r->sc[2 * b + 1] * hi;
     const float sa = asc[(size_t)b * M_stride + m];
     float v;
     if (type == QREF_Q4_K) {
@@ -260,7 +287,7 @@ int qref_blockdot(int type, const uint8_t* W, int N, int K, const int8_t* aq, co
   {
     row_dec r;
     r.q = (int8_t*)malloc((size_t)K);
-    r.sc = (int*)malloc(sizeof(int) * nb);
+    r.sc = (int*)malloc(sizeof(int) * 2 * nb);
     r.mn = (int*)malloc(sizeof(int) * nb);
     r.d = (float*)malloc(sizeof(float) * nb);
     r.dmin = (float*)malloc(sizeof(float) * nb);
@@ -359,7 +386,7 @@ int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_
     row_dec r;
     const int KM = E > F ? E : F;
     r.q = (int8_t*)malloc((size_t)KM);
-    r.sc = (int*)malloc(sizeof(int) * KM / 32);
+    r.sc = (int*)malloc(sizeof(int) * KM / 16);
     r.mn = (int*)malloc(sizeof(int) * KM / 32);
     r.d = (float*)malloc(sizeof(float) * KM / 32);
     r.dmin = (float*)malloc(sizeof(float) * KM / 32);

@@ -18,19 +18,22 @@ extern "C" {
 #endif
 
 /* GGML type ids (src/gguf.h:20-27) */
-enum { QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_IQ3_S = 21, QREF_IQ4_XS = 23 };
+enum { QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q6_K = 14, QREF_IQ3_S = 21, QREF_IQ4_XS = 23 };
 
 /* A decoded 256-element superblock: integer quants plus the per-type scales.
  *   Q8_0:   w[e] = d8[e/32] * q[e]
  *   Q4_K:   w[e] = d * sc[e/32] * q[e] - dmin * mn[e/32]
  *   IQ4_XS: w[e] = d * sc[e/32] * q[e]   (sc = ls - 32, q = kvalues_iq4nl[nibble])
- *   IQ3_S:  w[e] = d * sc[e/32] * q[e]   (sc = 1 + 2 * nibble, q = +-grid byte) */
+ *   IQ3_S:  w[e] = d * sc[e/32] * q[e]   (sc = 1 + 2 * nibble, q = +-grid byte)
+ *   Q6_K:   w[e] = d * sc16[e/16] * q[e]  (q = 6-bit value - 32; sc16 signed int8 per 16)
+ * sc16[i] is the integer scale of elements 16i..16i+15 for every type (sc16[2b] = sc16[2b+1] = sc[b] except Q6_K). */
 typedef struct {
   float d, dmin;
   float d8[8];
   int sc[8];
   int mn[8];
   int16_t q[256];
+  int sc16[16];
 } qref_sb;
 
 float qref_fp16_to_f32(uint16_t h);

@@ -1,6 +1,7 @@
 """Independent numpy encoders of the four GGUF block structs, written from the GGML block definitions
 (ggml-common.h: block_q8_0 {d; qs[32]}, block_q4_K {d; dmin; scales[12]; qs[128]}, block_iq4_xs {d; scales_h;
-scales_l[4]; qs[128]}, block_iq3_s {d; qs[64]; qh[8]; signs[32]; scales[4]}), NOT from the oracle's decoders: they
+scales_l[4]; qs[128]}, block_iq3_s {d; qs[64]; qh[8]; signs[32]; scales[4]}, block_q6_k {ql[128]; qh[64];
+scales[16]; d}), NOT from the oracle's decoders: they
 pack chosen integer fields into bytes, so decoding them back pins the decoders' bit positions."""
 import numpy as np
 
@@ -63,3 +64,18 @@ def enc_iq3_s(d, scale_nib, gidx, sign):
     for ib in range(8):
         sc[ib // 2] |= (scale_nib[ib] & 0xF) << (4 * (ib % 2))
     return np.concatenate([_h(d), qs, qh, signs, sc])
+
+
+def enc_q6_k(d, sc16, q):
+    """sc16: 16 int8 scales (one per 16 elements), q: 256 ints 0..63 (the stored 6-bit values) -> 210 bytes.
+    Element 128n + 32c + l (c = 0..3): low 4 bits in ql[64n + l + 32 (c & 1)], nibble c >> 1; high 2 bits in
+    qh[32n + l], bits 2c..2c+1."""
+    ql = np.zeros(128, dtype=np.uint8)
+    qh = np.zeros(64, dtype=np.uint8)
+    for n in range(2):
+        for c in range(4):
+            for l in range(32):
+                v = int(q[128 * n + 32 * c + l])
+                ql[64 * n + l + 32 * (c & 1)] |= (v & 0xF) << (4 * (c >> 1))
+                qh[32 * n + l] |= ((v >> 4) & 3) << (2 * c)
+    return np.concatenate([ql, qh, np.asarray(sc16, dtype=np.int8).view(np.uint8), _h(d)])

@@ -2,7 +2,7 @@
 
 Every expected value here is computed from the chosen integer FIELDS of each block (scales, nibbles, grid indices,
 sign bits) with numpy, following the GGML block definitions and the reference's per-element formulas
-(src/quants.h:149-158 Q8_0, 91-114 Q4_K, 297-312 IQ4_XS, 240-262 IQ3_S; quantizer 559-576; GEMV per-block
+(src/quants.h:149-158 Q8_0, 91-114 Q4_K, 125-141 Q6_K, 297-312 IQ4_XS, 240-262 IQ3_S; quantizer 559-576; GEMV per-block
 expression zero/kernels/decode.cl:695-706). Nothing here calls the oracle or the product, so the fixture pins both.
 The block bytes come from tests/encoders.py (packing written from the GGML structs).
 
@@ -48,6 +48,17 @@ def superblocks(qtype, rng, grid):
             sc, mn = np.ones(8, np.int64), np.zeros(8, np.int64)
             dq = (d8.astype(F32)[e] * q.astype(F32)).astype(F32)
             out.append((raw, q, sc, mn, d8.astype(F32), F32(0), dq))
+            continue
+        if qtype == 14:  # Q6_K: per-16 int8 scales, 6-bit q stored with an offset of 32
+            sc16 = rng.integers(-128, 128, 16)
+            q6 = rng.integers(0, 64, 256)
+            if i == 1:
+                q6[:] = 63
+                sc16[:] = -128
+            raw = enc.enc_q6_k(d, sc16, q6)
+            e16 = np.arange(256) // 16
+            dq = ((F32(d) * sc16[e16].astype(F32)) * (q6 - 32).astype(F32)).astype(F32)
+            out.append((raw, q6 - 32, sc16, np.zeros(8, np.int64), F32(d), F32(0), dq))
             continue
         if qtype == 12:  # Q4_K
             dmin = np.float16(D_EDGE[(i + 1) % len(D_EDGE)]) if i < len(D_EDGE) else np.float16(abs(rng.standard_normal()) * 0.01)
@@ -123,7 +134,7 @@ def main():
     data.update(quant_x=x, quant_aq=aq, quant_asc=asc, quant_absum=absum)
     # per type: edge + random superblocks as an N x K matrix (N = 16 rows of K = 512), its dequantized values,
     # the int32 block sums against the first quantizer row pattern, and the GEMV output
-    for qtype, name in ((8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s")):
+    for qtype, name in ((8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k")):
         sbs = superblocks(qtype, rng, grid)
         N, K = 16, 512
         nsb = K // 256
@@ -141,7 +152,11 @@ def main():
                 for j in range(8):
                     b = 8 * s + j
                     a = aq1[0, 32 * b:32 * b + 32].astype(np.int64)
-                    iv = int(sc[j]) * int(np.dot(q[32 * j:32 * j + 32].astype(np.int64), a))
+                    qq = q[32 * j:32 * j + 32].astype(np.int64)
+                    if qtype == 14:  # sc0 * lo + sc1 * hi
+                        iv = int(sc[2 * j]) * int(np.dot(qq[:16], a[:16])) + int(sc[2 * j + 1]) * int(np.dot(qq[16:], a[16:]))
+                    else:
+                        iv = int(sc[j]) * int(np.dot(qq, a))
                     isum[n, b] = iv
                     sa = asc1[b, 0]
                     if qtype == 8:

@@ -10,7 +10,7 @@ import pytest
 import oracle
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.npz")
-TYPES = [(8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s")]
+TYPES = [(8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k")]
 K = 512
 
 
@@ -64,7 +64,7 @@ def test_gpu_gemv_known_answers(g, qm, dev, qtype, name):
     isum, msum = qm.gemv_blocksums(w, aq, absum)
     y = qm.gemv(w, aq, asc, absum)
     # the prompt GEMM on the same row (M = 16 padded rows; row 0 is the token)
-    ygemm = qm.gemm(w, aq, asc, absum, M=16)
+    ygemm = qm.gemm(w, aq, asc, absum, M=16) if qtype != 14 else None
     torch.cuda.synchronize()
     assert np.array_equal(isum.cpu().numpy()[0].astype(np.int64), g[f"{name}_isum"])
     if qtype == 12:
@@ -72,5 +72,6 @@ def test_gpu_gemv_known_answers(g, qm, dev, qtype, name):
     ref = g[f"{name}_y"]
     scale = np.max(np.abs(ref))
     assert np.max(np.abs(y.cpu().numpy()[0] - ref)) <= 1e-4 * scale
-    assert np.max(np.abs(ygemm.cpu().numpy()[0] - ref)) <= 1e-4 * scale
+    if ygemm is not None:
+        assert np.max(np.abs(ygemm.cpu().numpy()[0] - ref)) <= 1e-4 * scale
     w.release()

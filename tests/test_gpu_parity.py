@@ -14,6 +14,7 @@ pytestmark = pytest.mark.gpu
 TOL_INT8_PATH = 1e-4
 TOL_F32_REF = 1e-3
 TYPES = [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S]
+GEMV_TYPES = TYPES + [F.Q6_K]
 
 
 def rel_err(got, ref):
@@ -64,7 +65,7 @@ def test_quantizer_strided_input(qm, dev):
 
 
 # ---- (b) decode GEMV
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (48, 768, 3), (40, 8192, 1), (16, 256, 8)])
 def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
     rng = np.random.default_rng(qtype + N + K)
@@ -80,7 +81,7 @@ def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
         assert np.array_equal(msum.cpu().numpy(), rmsum)
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (200, 2048, 1), (72, 17408, 1), (96, 5120, 2), (64, 1536, 5)])
 def test_gemv_f32_parity(qm, dev, qtype, N, K, T):
     import torch

@@ -131,7 +131,7 @@ def test_iq3_s_decoder_round_trip():
         assert np.array_equal(w, ref)
 
 
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
 def test_synth_weights_have_the_requested_statistics(qtype):
     W = F.synth_weight(qtype, 64, 512, seed=5)
     assert W.shape == (64, F.row_bytes(qtype, 512))
@@ -140,3 +140,20 @@ def test_synth_weights_have_the_requested_statistics(qtype):
     if qtype == F.Q8_0:
         q = W.reshape(-1, 34)[:, 2:].view(np.int8)
         assert q.min() >= -127 and q.max() <= 127
+
+
+def test_q6_k_decoder_round_trip():
+    rng = np.random.default_rng(5)
+    for it in range(40):
+        d = np.float16(rng.standard_normal())
+        sc16 = rng.integers(-128, 128, 16)
+        q = rng.integers(0, 64, 256)
+        if it == 0:
+            q[:] = 63
+            sc16[:] = -128
+        raw = enc.enc_q6_k(d, sc16, q)
+        o = oracle.decode_sb(F.Q6_K, raw)
+        assert np.array_equal(o["q"], q - 32) and np.array_equal(o["sc16"], sc16) and o["d"] == np.float32(d)
+        w = oracle.dequant_rows(F.Q6_K, raw[None], 256)[0]
+        ref = (np.float32(d) * sc16[np.arange(256) // 16].astype(np.float32) * (q - 32).astype(np.float32))
+        assert np.array_equal(w, ref.astype(np.float32))

@@ -69,7 +69,7 @@ def test_quantize_layout_padding_and_absum():
 
 
 # ---- int8 block-dot products
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
 def test_blockdot_int_sums_brute_force(qtype):
     rng = np.random.default_rng(10 + qtype)
     N, K, M = 12, 512, 3
@@ -81,17 +81,18 @@ def test_blockdot_int_sums_brute_force(qtype):
     for n in range(N):
         sbs = [oracle.decode_sb(qtype, W[n, s * F.SB_BYTES[qtype]:(s + 1) * F.SB_BYTES[qtype]]) for s in range(K // 256)]
         q = np.concatenate([s["q"] for s in sbs])
-        sc = np.concatenate([s["sc"] for s in sbs])
+        sc16 = np.concatenate([s["sc16"] for s in sbs])
         mn = np.concatenate([s["mn"] for s in sbs])
         for m in range(M):
-            prod = (q * aq[m].astype(np.int64)).reshape(nb, 32).sum(axis=1)
-            assert np.array_equal(isum[m, n], sc * prod)
+            # per 16-element half: sc0 * lo + sc1 * hi (decode.cl:695-706)
+            prod16 = (q * aq[m].astype(np.int64)).reshape(2 * nb, 16).sum(axis=1)
+            assert np.array_equal(isum[m, n], (sc16 * prod16).reshape(nb, 2).sum(axis=1))
             if qtype == F.Q4_K:
                 bs = aq[m].astype(np.int64).reshape(nb, 32).sum(axis=1)
                 assert np.array_equal(msum[m, n], mn * bs)
 
 
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
 def test_blockdot_f32_vs_dequantized_double(qtype):
     rng = np.random.default_rng(20 + qtype)
     N, K, M = 40, 1024, 4
