@@ -326,8 +326,6 @@ int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const i
                  float* C, int ldc, int c_off, int accumulate, void* stream) {
   if (int st = check_acts("qmatmul_gemm", w, aq, asc, absum, M, M_stride)) return st;
   if (!C) return fail(QM_ERR_ARG, "qmatmul_gemm: null output");
-  if (w->type == QM_Q6_K)
-    return fail(QM_ERR_TYPE, "qmatmul_gemm: Q6_K has no prompt GEMM yet (qmatmul_gemv takes it, 8 tokens per call)");
   if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm: rows %d not a multiple of 16", w->rows);
   if (accumulate < 0 || accumulate > 2) return fail(QM_ERR_ARG, "qmatmul_gemm: accumulate %d (0..2)", accumulate);
   if (c_off < 0 || ldc < c_off + w->rows)
@@ -352,7 +350,6 @@ int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_st
   static const float unused = 0.0f;  // (the block-sum mode reads no scales or sums)
   if (int st = check_acts("qmatmul_gemm_blocksums", w, aq, &unused, (const int16_t*)&unused, M, M_stride)) return st;
   if (!isum) return fail(QM_ERR_ARG, "qmatmul_gemm_blocksums: null output");
-  if (w->type == QM_Q6_K) return fail(QM_ERR_TYPE, "qmatmul_gemm_blocksums: Q6_K has no prompt GEMM yet");
   if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm_blocksums: rows %d not a multiple of 16", w->rows);
   QM_CHECK_INIT();
   qm::GemmArgs a{};

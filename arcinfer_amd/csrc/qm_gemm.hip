@@ -446,6 +446,175 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Q6_K prompt GEMM. Q6_K has an integer scale per 16 elements, so each 32-block needs its two halves' int32 sums
+// separately (the reference's sc0 * lo + sc1 * hi): two v_mfma_i32_32x32x16_i8 per block and row tile, lane half h
+// holding elements 8h..8h+7 of each 16-element half. The B operand is decoded in registers to signed int8 (the 6-bit
+// value minus 32, a byte-wise subtract without borrows); one 2-block f32 outer product gives asc * d * sc for both
+// halves (lanes 0-31: the first half's scale, lanes 32-63: the second's). Tiles, staging and epilogue as
+// gemm_kernel's dense mode.
+template <int MT, bool DUMP>
+__global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
+  constexpr int BM = 32 * MT;
+  constexpr int ACH = BM * 16 / 256;
+  constexpr int SCH = (8 * BM + 255) / 256;
+  using Tr = Traits<T_Q6_K>;
+  __shared__ GemmLds<T_Q6_K, MT> L;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
+  const int K = a.w.K, nb = K / 32, nsb = K / 256;
+  int nt, mtile;
+  dense_tile(nt, mtile);
+  const int m0 = mtile * BM, nvalid = min(BM, a.M - m0);
+  const int n_loc = nt * 128 + wave * 32 + lc, n_rows = a.w.rows;
+  const int n = min(n_loc, n_rows - 1);
+  if (tid < BM) L.arow[tid] = m0 + min(tid, nvalid - 1);
+  const uint32_t hfm = 0u - (uint32_t)hf;
+  __syncthreads();
+
+  u32x4_t st_a[ACH];
+  float st_sc[SCH];
+  auto fetch = [&](int sb) {
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;
+      st_a[c] = *(const u32x4_t*)(a.aq + (size_t)L.arow[row] * K + sb * 256 + col * 16);
+    }
+    if constexpr (!DUMP) {
+#pragma unroll
+      for (int c = 0; c < SCH; ++c) {
+        const int idx = min(tid + 256 * c, 8 * BM - 1), blk = idx / BM, src = L.arow[idx % BM];
+        st_sc[c] = a.asc[(size_t)(sb * 8 + blk) * a.M_stride + src];
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const int ch = tid + 256 * c, row = ch >> 4, col = ch & 15;
+      *(u32x4_t*)(L.a[buf] + row * A_STRIDE + col * 16) = st_a[c];
+    }
+    if constexpr (!DUMP) {
+#pragma unroll
+      for (int c = 0; c < SCH; ++c) {
+        const int idx = tid + 256 * c;
+        if (idx < 8 * BM) L.asc[buf][idx] = st_sc[c];
+      }
+    }
+  };
+  // this lane's share of a block: nibble bytes 8h..8h+7 and both 2-bit words (record: 16 nibble bytes, 2 words)
+  const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
+  const uint8_t* hrow = a.w.hdr + (size_t)n * nsb * Tr::HB;
+  auto load_blk = [&](int blk, uint2& nib, uint2& hw) {
+    const uint8_t* r = qrow + (size_t)blk * Tr::QB;
+    nib = *(const uint2*)(r + 8 * hf);
+    hw = *(const uint2*)(r + 16);
+  };
+  uint2 nib[8], hw[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) load_blk(b, nib[b], hw[b]);
+  // (header records are 20 bytes: 4-byte aligned, so read as dwords)
+  auto load_hdr = [&](int sb, uint4& sc, uint32_t& dd) {
+    const uint32_t* h = (const uint32_t*)(hrow + (size_t)sb * Tr::HB);
+    sc = make_uint4(h[0], h[1], h[2], h[3]);  // int8 scales[16]
+    dd = h[4];                                // f16 d
+  };
+  uint4 hsc;
+  uint32_t hd;
+  load_hdr(0, hsc, hd);
+  v16f acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
+  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v32f zero32;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) zero32[r] = 0.0f;
+  fetch(0);
+  store(0);
+  __syncthreads();
+
+  for (int s = 0; s < nsb; ++s) {
+    const int cur = s & 1;
+    const int sn = s + 1 < nsb ? s + 1 : s;
+    fetch(sn);
+    const uint32_t scw[4] = {hsc.x, hsc.y, hsc.z, hsc.w};
+    const float d = h2f(hd);
+    load_hdr(sn, hsc, hd);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (b == 4) store(cur ^ 1);
+      // B operands: elements 8hf..8hf+7 of the block's first half (o0) and of its second half (o1), signed
+      const uint32_t A2 = hf ? hw[b].x : hw[b].x << 4, B2 = hf ? hw[b].y : hw[b].y << 4;
+      uint32_t w[4];
+      w[0] = (nib[b].x & 0x0F0F0F0Fu) | (A2 & 0x30303030u);
+      w[1] = (nib[b].y & 0x0F0F0F0Fu) | ((A2 >> 2) & 0x30303030u);
+      w[2] = ((nib[b].x >> 4) & 0x0F0F0F0Fu) | (B2 & 0x30303030u);
+      w[3] = ((nib[b].y >> 4) & 0x0F0F0F0Fu) | ((B2 >> 2) & 0x30303030u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = ((w[k] | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+      const long o0 = (long)(((uint64_t)w[1] << 32) | w[0]), o1 = (long)(((uint64_t)w[3] << 32) | w[2]);
+      load_blk(sn * 8 + b, nib[b], hw[b]);
+      const int sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
+      const int sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
+      const float my_dsc = d * (float)(hf ? sc1 : sc0);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t* ar = L.a[cur] + (mt * 32 + lc) * A_STRIDE + 32 * b + 8 * hf;
+        const long a0 = *(const long*)ar, a1 = *(const long*)(ar + 16);
+        const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, o0, zero16, 0, 0, 0);
+        const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, o1, zero16, 0, 0, 0);
+        if constexpr (DUMP) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (i < nvalid && n_loc < n_rows)
+              a.dbg_isum[((size_t)(m0 + i) * n_rows + n_loc) * nb + s * 8 + b] = sc0 * d0[r] + sc1 * d1[r];
+          }
+        } else {
+          const float my_asc = L.asc[cur][b * BM + mt * 32 + lc];
+          const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            acc[mt][r] = fmaf(sc[r], (float)d0[r], acc[mt][r]);
+            acc[mt][r] = fmaf(sc[16 + r], (float)d1[r], acc[mt][r]);
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+  }
+  if constexpr (DUMP) return;
+  const bool col_ok = n_loc < n_rows;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (i < nvalid && col_ok) {
+        float* cp = a.C + (size_t)(m0 + i) * a.ldc + a.c_off + n_loc;
+        float v = acc[mt][r];
+        if (a.accumulate == 1) {
+          v += *cp;
+        } else if (a.accumulate == 2) {
+          const float g = *cp;
+          v *= g / (1.0f + expf(-g));
+        }
+        *cp = v;
+      }
+    }
+}
+
+template <int MT, bool DUMP>
+static hipError_t go_q6k(const GemmArgs& a, hipStream_t s) {
+  const unsigned gx = (unsigned)((a.w.rows + 127) / 128), gy = (unsigned)((a.M + 32 * MT - 1) / (32 * MT));
+  gemm_q6k_kernel<MT, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
+  return hipGetLastError();
+}
+
 template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go(const GemmArgs& a, hipStream_t s) {
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
@@ -473,6 +642,11 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
+  if (type == T_Q6_K) {
+    if (mode != GEMM_DENSE) return hipErrorInvalidValue;
+    if (a.dbg_isum) return go_q6k<1, true>(a, s);
+    return a.M <= 32 ? go_q6k<1, false>(a, s) : go_q6k<2, false>(a, s);
+  }
   switch (type) {
     case T_Q8_0: return dispatch<T_Q8_0>(mode, a, s);
     case T_Q4_K: return dispatch<T_Q4_K>(mode, a, s);

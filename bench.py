@@ -223,6 +223,12 @@ def main():
             g["cpu_baseline"] = {"value": round(ops / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthreads,
                                  "kind": "port", "sample": f"every {stride}th output column of the same GEMM "
                                                            f"(oracle/qref.c int8 block-dot), time x {stride}"}
+        # the same prompt GEMM with Q6_K weights (per-16 scales: two K=16 MFMAs per block), reported
+        W6 = F.synth_weight(F.Q6_K, N, K, seed=6)
+        w6 = qm.QWeight(F.Q6_K, torch.from_numpy(W6).to(dev), N, K)
+        ms6, _ = timed(lambda i: qm.gemm(w6, aq, asc, absum, C=C, ldc=N), steps, args.warmup, stream)
+        g["q6_k"] = {"TOPS": round(ops / (ms6 * 1e-3) / 1e12, 1), "ms_per_launch": round(ms6, 4)}
+        w6.release()
         out["gemm"] = g
         w.release()
         del C, x, aq, asc, absum

@@ -64,7 +64,7 @@ def test_gpu_gemv_known_answers(g, qm, dev, qtype, name):
     isum, msum = qm.gemv_blocksums(w, aq, absum)
     y = qm.gemv(w, aq, asc, absum)
     # the prompt GEMM on the same row (M = 16 padded rows; row 0 is the token)
-    ygemm = qm.gemm(w, aq, asc, absum, M=16) if qtype != 14 else None
+    ygemm = qm.gemm(w, aq, asc, absum, M=16)
     torch.cuda.synchronize()
     assert np.array_equal(isum.cpu().numpy()[0].astype(np.int64), g[f"{name}_isum"])
     if qtype == 12:
@@ -72,6 +72,5 @@ def test_gpu_gemv_known_answers(g, qm, dev, qtype, name):
     ref = g[f"{name}_y"]
     scale = np.max(np.abs(ref))
     assert np.max(np.abs(y.cpu().numpy()[0] - ref)) <= 1e-4 * scale
-    if ygemm is not None:
-        assert np.max(np.abs(ygemm.cpu().numpy()[0] - ref)) <= 1e-4 * scale
+    assert np.max(np.abs(ygemm.cpu().numpy()[0] - ref)) <= 1e-4 * scale
     w.release()

@@ -150,7 +150,7 @@ def test_gemv_baseline_iq4_xs(qm, dev, N, K):
 
 
 # ---- (c) prompt GEMM on int8 MFMA
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("M,N,K", [(32, 128, 512), (37, 144, 768)])
 def test_gemm_blocksums_bit_exact(qm, dev, qtype, M, N, K):
     rng = np.random.default_rng(M + N + qtype)
@@ -164,7 +164,7 @@ def test_gemm_blocksums_bit_exact(qm, dev, qtype, M, N, K):
     assert np.array_equal(isum.cpu().numpy(), risum)
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("M,Ms,N,K", [(64, 64, 256, 1024), (100, 128, 384, 2048), (16, 16, 128, 256),
                                       (130, 130, 512, 5120)])
 def test_gemm_f32_parity(qm, dev, qtype, M, Ms, N, K):
