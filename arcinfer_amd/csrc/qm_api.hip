@@ -34,9 +34,12 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(QM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-bool known_type(int t) { return t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q6_K || t == QM_IQ3_S || t == QM_IQ4_XS; }
+bool known_type(int t) {
+  return t == QM_Q4_0 || t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q5_K || t == QM_Q6_K || t == QM_IQ4_NL || t == QM_IQ3_S ||
+         t == QM_IQ4_XS;
+}
 
-int payload_bytes(int t) { return t == QM_Q8_0 ? 32 : t == QM_IQ3_S ? 12 : t == QM_Q6_K ? 24 : 16; }
+int payload_bytes(int t) { return t == QM_Q8_0 ? 32 : t == QM_IQ3_S ? 12 : t == QM_Q6_K ? 24 : t == QM_Q5_K ? 20 : 16; }
 int header_bytes(int t) { return t == QM_IQ4_XS ? 8 : t == QM_Q6_K ? 20 : 16; }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -127,6 +130,9 @@ size_t qmatmul_sb_bytes(int type) {
     case QM_Q8_0: return 272;
     case QM_Q4_K: return 144;
     case QM_Q6_K: return 210;
+    case QM_Q5_K: return 176;
+    case QM_Q4_0: return 144;
+    case QM_IQ4_NL: return 144;
     case QM_IQ3_S: return 110;
     case QM_IQ4_XS: return 136;
     default: return 0;
@@ -271,8 +277,8 @@ int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, floa
 static int check_acts(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
                       int rows_needed, int M_stride) {
   if (!w || !aq || !asc) return fail(QM_ERR_ARG, "%s: null pointer", fn);
-  if ((w->type == QM_Q4_K || w->type == QM_Q6_K) && !absum)
-    return fail(QM_ERR_ARG, "%s: Q4_K and Q6_K need the per-16 activation sums", fn);
+  if ((w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K) && !absum)
+    return fail(QM_ERR_ARG, "%s: Q4_K, Q5_K and Q6_K need the per-16 activation sums", fn);
   if (rows_needed < 1 || M_stride < rows_needed)
     return fail(QM_ERR_SHAPE, "%s: %d activation rows with M_stride %d", fn, rows_needed, M_stride);
   if (!aligned(aq, 16)) return fail(QM_ERR_ARG, "%s: aq must be 16-byte aligned", fn);
@@ -307,7 +313,8 @@ int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* 
                            int32_t* isum, int32_t* msum, void* stream) {
   static const float unused = 0.0f;  // (the block-sum mode reads no scales)
   if (int st = check_acts("qmatmul_gemv_blocksums", w, aq, &unused, absum, T, M_stride)) return st;
-  if (!isum || (w->type == QM_Q4_K && !msum)) return fail(QM_ERR_ARG, "qmatmul_gemv_blocksums: null output");
+  if (!isum || ((w->type == QM_Q4_K || w->type == QM_Q5_K) && !msum))
+    return fail(QM_ERR_ARG, "qmatmul_gemv_blocksums: null output");
   if (T < 1 || T > 8) return fail(QM_ERR_SHAPE, "qmatmul_gemv_blocksums: T = %d", T);
   QM_CHECK_INIT();
   qm::GemvArgs a{};
@@ -410,8 +417,8 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
   for (const qm_weight* w : {gate, up, down})
-    if (w->type == QM_Q4_K || w->type == QM_Q6_K)
-      return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: Q4_K and Q6_K expert weights (per-16 sums) are not supported");
+    if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K)
+      return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: Q4_K, Q5_K and Q6_K expert weights (per-16 sums) are not supported");
   if (gate->type != up->type)
     return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: gate and up must have one type (got %d, %d)", gate->type, up->type);
   if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)

@@ -8,7 +8,7 @@ namespace qm {
 template <int TYPE> struct LdsFor { struct type { int unused; }; };
 template <> struct LdsFor<T_IQ3_S> { using type = Iq3Lds; };
 
-// The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0 also q1) and header (h).
+// The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0, Q5_K and Q6_K also q1) and header (h).
 // (native vector members: arrays of structs holding HIP's uint4 are kept in scratch memory)
 struct RawBlk {
   u32x4_t q0, q1, h;
@@ -27,6 +27,13 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
     r.q0 = ld_stream16(qp);
     r.q1 = ld_stream16(qp + 16);
     r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
+    r.q0 = ld_stream16(qp);
+    r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (TYPE == T_Q5_K) {
+    r.q0 = ld_stream16(qp);
+    r.q1.x = __builtin_nontemporal_load((const uint32_t*)(qp + 16));
+    r.h = *(const u32x4_t*)hp;
   } else if constexpr (TYPE == T_Q6_K) {
     r.q0 = ld_stream16(qp);
     const uint32_t* q = (const uint32_t*)(qp + 16);
@@ -87,12 +94,43 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     wd[4] = r.q1.x; wd[5] = r.q1.y; wd[6] = r.q1.z; wd[7] = r.q1.w;
     d = h2f(r.h.x);
     sc = 1;
-  } else if constexpr (TYPE == T_Q4_K) {
+  } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
     const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      wd[k] = qq[k] & 0x0F0F0F0Fu;
-      wd[4 + k] = (qq[k] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (TYPE == T_Q4_0) {
+        wd[k] = sub8_bytes(qq[k] & 0x0F0F0F0Fu);
+        wd[4 + k] = sub8_bytes((qq[k] >> 4) & 0x0F0F0F0Fu);
+      } else {
+        wd[k] = kv_lookup4(kv, qq[k] & 0x0F0F0F0Fu);
+        wd[4 + k] = kv_lookup4(kv, (qq[k] >> 4) & 0x0F0F0F0Fu);
+      }
+    }
+    d = h2f(r.h.x);
+    sc = 1;
+  } else if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+    const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
+    if constexpr (TYPE == T_Q4_K) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        wd[k] = qq[k] & 0x0F0F0F0Fu;
+        wd[4 + k] = (qq[k] >> 4) & 0x0F0F0F0Fu;
+      }
+    } else {
+      // half h's 16 nibbles in words 2h, 2h+1 (low nibbles: its elements 0-7, high: 8-15), fifth bits in q1.x
+      wd[0] = r.q0.x & 0x0F0F0F0Fu;
+      wd[1] = r.q0.y & 0x0F0F0F0Fu;
+      wd[2] = (r.q0.x >> 4) & 0x0F0F0F0Fu;
+      wd[3] = (r.q0.y >> 4) & 0x0F0F0F0Fu;
+      wd[4] = r.q0.z & 0x0F0F0F0Fu;
+      wd[5] = r.q0.w & 0x0F0F0F0Fu;
+      wd[6] = (r.q0.z >> 4) & 0x0F0F0F0Fu;
+      wd[7] = (r.q0.w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        wd[k] |= ((r.q1.x >> k) & 0x01010101u) << 4;
+        wd[4 + k] |= ((r.q1.x >> (4 + k)) & 0x01010101u) << 4;
+      }
     }
     d = h2f(r.h.x);
     dmin = h2f(r.h.x >> 16);
@@ -119,7 +157,8 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
 }
 
 // One 32-block's integer products with one token's int8 activations (x0: elements 0-15, x1: 16-31; bs0 / bs1 their
-// per-16 sums, used by Q4_K and Q6_K): iv = sc0 * lo + sc1 * hi over the signed quants and, for Q4_K, the min term
+// per-16 sums, used by Q4_K, Q5_K and Q6_K): iv = sc0 * lo + sc1 * hi over the signed quants and, for Q4_K / Q5_K,
+// the min term
 // mv = mn * (bs0 + bs1) -- the reference's per-block integers (zero/kernels/decode.cl:695-706). Q6_K's stored
 // values q carry an offset of 32: sum a * (q - 32) = lo - 32 * bs.
 struct BlockInts {
@@ -142,7 +181,7 @@ __device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1,
   if constexpr (Traits<TYPE>::SC16) {
     // (|lo - 32 bs| < 2^17 and |sc| < 2^7: the 24-bit multiplies are exact)
     iv = __mul24(sc, lo - 32 * bs0) + __mul24(sc1, hi - 32 * bs1);
-  } else if constexpr (TYPE == T_Q8_0) {
+  } else if constexpr (kBlockScales<TYPE>) {
     iv = lo + hi;
   } else {
     iv = __mul24(sc, lo + hi);

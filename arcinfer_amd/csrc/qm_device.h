@@ -9,6 +9,10 @@
 //   Q4_K   QB 16: byte t = q[t] | q[16+t] << 4       HB 16: f16 d, f16 dmin, 12 bytes of 6-bit scales/mins (GGUF)
 //   IQ4_XS QB 16: byte t = i[t] | i[16+t] << 4       HB  8: f16 d, u16 scales_h, u8 scales_l[4] (GGUF)
 //   IQ3_S  QB 12: 8 index low bytes, 4 sign bytes    HB 16: qh[8], scales[4], f16 d, 2 bytes zero
+//   Q5_K   QB 20: per 16-element half h, 8 bytes: byte t = low4[16h+t] | low4[16h+8+t] << 4 (a prompt-GEMM lane
+//                 loads only its half), then a word of fifth bits: byte i, bit k = bit4[4k+i], bit 4+k = bit4[16+4k+i]
+//                 HB 16: as Q4_K
+//   Q4_0, IQ4_NL QB 16: byte t = n[t] | n[16+t] << 4 (GGUF order)       HB 16: the 8 blocks' f16 scales (as Q8_0)
 //   Q6_K   QB 24: byte t = low4[t] | low4[16+t] << 4, then two words of 2-bit high parts: word h (h = 0, 1),
 //                 byte i, bits 2k..2k+1 = high2[16h + 4k + i]          HB 20: int8 scales[16] (per 16), f16 d, 2 zero
 // (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
@@ -23,16 +27,21 @@
 
 namespace qm {
 
-enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_IQ3_S = 21, T_IQ4_XS = 23 };
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ4_XS = 23 };
 
 template <int TYPE> struct Traits;
 // MINS: per-block mins (the activation block sums enter the result); SC16: two integer scales per 32-block (one per
 // 16) and quants stored with an offset of 32 (removed with the per-16 activation sums)
 template <> struct Traits<T_Q8_0> { static constexpr int QB = 32, HB = 16, GGUF_SB = 272; static constexpr bool MINS = false, SC16 = false; };
 template <> struct Traits<T_Q4_K> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = true, SC16 = false; };
+template <> struct Traits<T_Q5_K> { static constexpr int QB = 20, HB = 16, GGUF_SB = 176; static constexpr bool MINS = true, SC16 = false; };
+template <> struct Traits<T_Q4_0> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false; };
+template <> struct Traits<T_IQ4_NL> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false; };
 template <> struct Traits<T_Q6_K> { static constexpr int QB = 24, HB = 20, GGUF_SB = 210; static constexpr bool MINS = false, SC16 = true; };
 template <> struct Traits<T_IQ4_XS> { static constexpr int QB = 16, HB = 8, GGUF_SB = 136; static constexpr bool MINS = false, SC16 = false; };
 template <> struct Traits<T_IQ3_S> { static constexpr int QB = 12, HB = 16, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false; };
+// per-32 f16 scales in the header (Q8_0's layout), no integer sub-scales
+template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL;
 // whether the kernels need the per-16 activation sums (absum)
 template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
 
@@ -178,4 +187,9 @@ __device__ __forceinline__ float wave_sum_width(float v, int width) {
   return v;
 }
 
+}  // namespace qm
+
+namespace qm {
+// n - 8 for four nibble values 0..15 held one per byte: a byte-wise subtract without borrows
+__device__ __forceinline__ uint32_t sub8_bytes(uint32_t n) { return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 }  // namespace qm

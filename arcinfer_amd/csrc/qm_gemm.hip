@@ -48,13 +48,17 @@ __device__ __forceinline__ void iq3s_pair_rt(const Iq3Lds* t, uint32_t q0, uint3
 }
 
 // A lane's payload of one 32-block (the bytes its k-half needs): 16 B for Q8_0 (its half of the 32 int8), the block's
-// 16 nibble bytes for Q4_K / IQ4_XS, the 8 index bytes + 4 sign bytes for IQ3_S (.w unused).
+// 16 nibble bytes for the other 4-bit types, Q5_K's 8 nibble bytes of its half and the word of fifth bits (.x .y
+// nibbles, .z fifth bits, .w unused), the 8 index bytes + 4 sign bytes for IQ3_S (.w unused).
 template <int TYPE>
 __device__ __forceinline__ uint4 load_payload(const WView& w, int n, int blk, int hf) {
   using Tr = Traits<TYPE>;
   const uint8_t* qp = w.qs + ((size_t)n * (w.K / 32) + blk) * Tr::QB;
   if constexpr (TYPE == T_Q8_0) {
     return *(const uint4*)(qp + 16 * hf);
+  } else if constexpr (TYPE == T_Q5_K) {
+    const uint2 nib = *(const uint2*)(qp + 8 * hf);
+    return make_uint4(nib.x, nib.y, *(const uint32_t*)(qp + 16), 0u);
   } else if constexpr (TYPE == T_IQ3_S) {
     const uint32_t* q = (const uint32_t*)qp;
     return make_uint4(q[0], q[1], q[2], 0u);
@@ -80,12 +84,22 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
   v4i r;
   if constexpr (TYPE == T_Q8_0) {
     r[0] = (int)q.x; r[1] = (int)q.y; r[2] = (int)q.z; r[3] = (int)q.w;
-  } else if constexpr (TYPE == T_Q4_K || TYPE == T_IQ4_XS) {
+  } else if constexpr (TYPE == T_Q5_K) {
+    // (fifth bits: byte i, bit k = element 4k+i of the first half, bit 4+k = of the second)
+    r[0] = (int)(q.x & 0x0F0F0F0Fu); r[1] = (int)(q.y & 0x0F0F0F0Fu);
+    r[2] = (int)((q.x >> 4) & 0x0F0F0F0Fu); r[3] = (int)((q.y >> 4) & 0x0F0F0F0Fu);
+    const uint32_t hb = q.z >> (4 * hf);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] |= (int)(((hb >> k) & 0x01010101u) << 4);
+  } else if constexpr (TYPE != T_IQ3_S) {
     const int sh = 4 * hf;
     const uint32_t x0 = q.x >> sh, x1 = q.y >> sh, x2 = q.z >> sh, x3 = q.w >> sh;
     if constexpr (TYPE == T_Q4_K) {
       r[0] = (int)(x0 & 0x0F0F0F0Fu); r[1] = (int)(x1 & 0x0F0F0F0Fu);
       r[2] = (int)(x2 & 0x0F0F0F0Fu); r[3] = (int)(x3 & 0x0F0F0F0Fu);
+    } else if constexpr (TYPE == T_Q4_0) {
+      r[0] = (int)sub8_bytes(x0 & 0x0F0F0F0Fu); r[1] = (int)sub8_bytes(x1 & 0x0F0F0F0Fu);
+      r[2] = (int)sub8_bytes(x2 & 0x0F0F0F0Fu); r[3] = (int)sub8_bytes(x3 & 0x0F0F0F0Fu);
     } else {
       r[0] = (int)kv_lookup4(kv, x0 & 0x0F0F0F0Fu); r[1] = (int)kv_lookup4(kv, x1 & 0x0F0F0F0Fu);
       r[2] = (int)kv_lookup4(kv, x2 & 0x0F0F0F0Fu); r[3] = (int)kv_lookup4(kv, x3 & 0x0F0F0F0Fu);
@@ -104,7 +118,7 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
 // dmn[b] = dmin * mn_b (Q4_K), isc[b] = the integer scale.
 template <int TYPE>
 __device__ __forceinline__ void sb_scales(uint4 h, float dsc[8], float dmn[8], int isc[8]) {
-  if constexpr (TYPE == T_Q8_0) {
+  if constexpr (kBlockScales<TYPE>) {
     const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -112,7 +126,7 @@ __device__ __forceinline__ void sb_scales(uint4 h, float dsc[8], float dmn[8], i
       dmn[b] = 0.0f;
       isc[b] = 1;
     }
-  } else if constexpr (TYPE == T_Q4_K) {
+  } else if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
     const float d = h2f(h.x), dmin = h2f(h.x >> 16);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -468,7 +482,6 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
   const int n_loc = nt * 128 + wave * 32 + lc, n_rows = a.w.rows;
   const int n = min(n_loc, n_rows - 1);
   if (tid < BM) L.arow[tid] = m0 + min(tid, nvalid - 1);
-  const uint32_t hfm = 0u - (uint32_t)hf;
   __syncthreads();
 
   u32x4_t st_a[ACH];
@@ -652,6 +665,9 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
     case T_Q4_K: return dispatch<T_Q4_K>(mode, a, s);
     case T_IQ4_XS: return dispatch<T_IQ4_XS>(mode, a, s);
     case T_IQ3_S: return dispatch<T_IQ3_S>(mode, a, s);
+    case T_Q4_0: return dispatch<T_Q4_0>(mode, a, s);
+    case T_IQ4_NL: return dispatch<T_IQ4_NL>(mode, a, s);
+    case T_Q5_K: return mode == GEMM_DENSE ? dispatch<T_Q5_K>(mode, a, s) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
 // LDS bytes of gemvs_kernel for TB tokens
 static size_t gemvs_lds(int type, int K, int TB) {
   const int nb = K / 32;
-  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q6_K ? sizeof(int) * nb : 0));
+  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
 }
 
 template <int TYPE, int LPR, int CH, bool EXACT, int TB>
@@ -409,6 +409,9 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_IQ4_XS: return dispatch<T_IQ4_XS>(a, s);
     case T_IQ3_S: return dispatch<T_IQ3_S>(a, s);
     case T_Q6_K: return dispatch<T_Q6_K>(a, s);
+    case T_Q5_K: return dispatch<T_Q5_K>(a, s);
+    case T_Q4_0: return dispatch<T_Q4_0>(a, s);
+    case T_IQ4_NL: return dispatch<T_IQ4_NL>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

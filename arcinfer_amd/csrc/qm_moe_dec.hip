@@ -186,6 +186,8 @@ hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const
     case T_Q8_0: return moe_dec_typed<T_Q8_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     case T_IQ4_XS: return moe_dec_typed<T_IQ4_XS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     case T_IQ3_S: return moe_dec_typed<T_IQ3_S>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_Q4_0: return moe_dec_typed<T_Q4_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ4_NL: return moe_dec_typed<T_IQ4_NL>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     default: return hipErrorInvalidValue;
   }
 }

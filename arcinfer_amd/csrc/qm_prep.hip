@@ -41,8 +41,37 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     // d, scales_h, scales_l[4] | qs[128] (block ib = qs[16 ib .. 16 ib + 15], already per-32)
     for (int e = 0; e < 8; ++e) h[e] = p[e];
     for (int e = 0; e < 128; ++e) q[e] = p[8 + e];
+  } else if constexpr (TYPE == T_Q5_K) {
+    // d, dmin, scales[12] | qh[32] | qs[128] (src/quants.h:91-114): chunk j's low / high nibbles are blocks 2j / 2j+1,
+    // their fifth bits bit 2j / 2j+1 of qh[l]
+    for (int e = 0; e < 16; ++e) h[e] = p[e];
+    const uint8_t *qh = p + 16, *src = p + 48;
+    for (int j = 0; j < 4; ++j)
+      for (int half = 0; half < 2; ++half) {
+        const int b = 2 * j + half;
+        uint8_t* dst = q + 20 * b;
+        uint8_t n[32], hb[32];
+        for (int l = 0; l < 32; ++l) {
+          n[l] = half ? (uint8_t)(src[32 * j + l] >> 4) : (uint8_t)(src[32 * j + l] & 0xF);
+          hb[l] = (uint8_t)((qh[l] >> b) & 1);
+        }
+        for (int hh = 0; hh < 2; ++hh)
+          for (int t = 0; t < 8; ++t) dst[8 * hh + t] = (uint8_t)(n[16 * hh + t] | (n[16 * hh + 8 + t] << 4));
+        for (int i = 0; i < 4; ++i) {
+          uint8_t v = 0;
+          for (int k = 0; k < 4; ++k) v |= (uint8_t)((hb[4 * k + i] << k) | (hb[16 + 4 * k + i] << (4 + k)));
+          dst[16 + i] = v;
+        }
+      }
+  } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
+    // 8 GGUF blocks of (f16 d, 16 nibble bytes)
+    for (int b = 0; b < 8; ++b) {
+      h[2 * b] = p[18 * b];
+      h[2 * b + 1] = p[18 * b + 1];
+      for (int t = 0; t < 16; ++t) q[16 * b + t] = p[18 * b + 2 + t];
+    }
   } else if constexpr (TYPE == T_Q6_K) {
-    // ql[128] | qh[64] | scales[16] | d (src/quants.h:125-141): element 128n + 32c + l has its low 4 bits in
+    // ql[128] | qh[64] | scales[16] | d (src/quants.h:115-135): element 128n + 32c + l has its low 4 bits in
     // ql[64n + l + 32 (c & 1)] (nibble c >> 1) and its high 2 bits in qh[32n + l] (bits 2c..2c+1); block b = 4n + c
     const uint8_t *ql = p, *qh = p + 128;
     for (int b = 0; b < 8; ++b) {
@@ -89,6 +118,9 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t*
     case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ4_NL: repack_kernel<T_IQ4_NL><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -1,17 +1,18 @@
 """GGUF block geometry of the weight types of the path, and seeded synthetic weights in GGUF block form.
 
-Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_K 256 / 144, Q6_K 256 / 210,
-IQ3_S 256 / 110, IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
+Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144,
+Q5_K 256 / 176, Q6_K 256 / 210, IQ3_S 256 / 110, IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
 bytes: every quant / index / sign / sub-scale bit uniform, the f16 super-scales |N(0, sigma)|.
 """
 import numpy as np
 
-Q8_0, Q4_K, Q6_K, IQ3_S, IQ4_XS = 8, 12, 14, 21, 23
-TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS = 2, 8, 12, 13, 14, 20, 21, 23
+TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S",
+              IQ4_XS: "IQ4_XS"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 # bytes of one 256-element superblock (Q8_0: 8 blocks of 34)
-SB_BYTES = {Q8_0: 272, Q4_K: 144, Q6_K: 210, IQ3_S: 110, IQ4_XS: 136}
+SB_BYTES = {Q4_0: 144, Q8_0: 272, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 144, IQ3_S: 110, IQ4_XS: 136}
 
 
 def row_bytes(qtype, K):
@@ -38,6 +39,8 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     IQ4_XS: nibbles and 6-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
     IQ3_S:  9-bit grid indices, signs and 4-bit sub-scales uniform, d = f16(|N(0, 0.01)|)
     Q6_K:   6-bit quants and int8 per-16 scales uniform, d = f16(|N(0, 0.01)|) (d is the last field)
+    Q5_K:   as Q4_K (the fifth bits uniform too)
+    Q4_0 / IQ4_NL: nibbles uniform, d = f16(|N(0, 0.02)| / 8) per 32
     """
     rng = np.random.default_rng(seed)
     nsb = K // 256
@@ -50,6 +53,14 @@ def synth_weight(qtype, N, K, seed, sigma=None):
         blk[:, 1] = d >> 8
         blk[:, 2:] = rng.integers(-127, 128, size=(nblk, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
         return blk.reshape(N, nsb * 272)
+    if qtype in (Q4_0, IQ4_NL):
+        sig = 0.02 if sigma is None else sigma
+        nblk = N * K // 32
+        blk = rng.integers(0, 256, size=(nblk, 18), dtype=np.uint8)
+        d = f16_bits(np.abs(rng.normal(0.0, sig, nblk)) / 8.0)
+        blk[:, 0] = d & 0xFF
+        blk[:, 1] = d >> 8
+        return blk.reshape(N, nsb * 144)
     sig = 0.01 if sigma is None else sigma
     sb = SB_BYTES[qtype]
     raw = rng.integers(0, 256, size=(N * nsb, sb), dtype=np.uint8)
@@ -57,7 +68,7 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     at = 208 if qtype == Q6_K else 0
     raw[:, at] = d & 0xFF
     raw[:, at + 1] = d >> 8
-    if qtype == Q4_K:
+    if qtype in (Q4_K, Q5_K):
         dm = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
         raw[:, 2] = dm & 0xFF
         raw[:, 3] = dm >> 8

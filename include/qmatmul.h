@@ -29,7 +29,9 @@ extern "C" {
 #endif
 
 /* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
-typedef enum { QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q6_K = 14, QM_IQ3_S = 21, QM_IQ4_XS = 23 } qm_type;
+typedef enum {
+  QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ4_XS = 23
+} qm_type;
 
 typedef enum {
   QM_OK = 0,
@@ -101,7 +103,7 @@ int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, floa
 
 /* Decode GEMV, T tokens (1..8) against one read of the weight:
  *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
- * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K and Q6_K.
+ * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K, Q5_K and Q6_K.
  * Replaces the gemv / gemv_v / gemv_mt / gemv_mt_v launches of Engine::matmul1 (zero/engine.h:3184-3232;
  * zero/kernels/decode.cl:636-737, 1074-1141, 1145-1411). */
 int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,

@@ -68,7 +68,10 @@ int qref_block_info(int type, int* blk, int* bytes) {
   switch (type) {
     case QREF_Q8_0: *blk = 32; *bytes = 34; return 0;
     case QREF_Q4_K: *blk = 256; *bytes = 144; return 0;
+    case QREF_Q5_K: *blk = 256; *bytes = 176; return 0;
     case QREF_Q6_K: *blk = 256; *bytes = 210; return 0;
+    case QREF_Q4_0: *blk = 32; *bytes = 18; return 0;
+    case QREF_IQ4_NL: *blk = 32; *bytes = 18; return 0;
     case QREF_IQ3_S: *blk = 256; *bytes = 110; return 0;
     case QREF_IQ4_XS: *blk = 256; *bytes = 136; return 0;
     default: return -1;
@@ -94,20 +97,46 @@ static void scale_min_k4(int j, const uint8_t* q, int* d, int* m) {
   }
 }
 
-/* src/quants.h:89-315 (cases Q4_K 91-114, Q8_0 149-158, IQ3_S 240-262, IQ4_XS 297-312) */
+/* src/quants.h:89-315 (cases Q4_K / Q5_K 91-114, Q6_K 115-135, Q4_0 136-148, Q8_0 149-158, IQ3_S 240-262,
+ * IQ4_XS 297-312; IQ4_NL from dequant_row 527-538) */
 static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
   memset(o, 0, sizeof(*o));
   switch (type) {
-    case QREF_Q4_K: {
+    case QREF_Q4_K:
+    case QREF_Q5_K: {
+      /* src/quants.h:91-114: d, dmin, 12 bytes of 6-bit scales/mins; Q5_K then qh[32] (bit 2j / 2j+1 of qh[l]: the
+       * fifth bit of elements 64j + l / 64j + 32 + l), then qs[128] */
       o->d = qref_fp16_to_f32(rd16(p));
       o->dmin = qref_fp16_to_f32(rd16(p + 2));
       for (int b = 0; b < 8; ++b) scale_min_k4(b, p + 4, &o->sc[b], &o->mn[b]);
-      const uint8_t* qs = p + 16;
+      const uint8_t* qh = type == QREF_Q5_K ? p + 16 : NULL;
+      const uint8_t* qs = type == QREF_Q5_K ? p + 48 : p + 16;
       for (int j = 0; j < 4; ++j)
         for (int l = 0; l < 32; ++l) {
-          o->q[64 * j + l] = (int16_t)(qs[32 * j + l] & 0xF);
-          o->q[64 * j + 32 + l] = (int16_t)(qs[32 * j + l] >> 4);
+          int lo = qs[32 * j + l] & 0xF, hi = qs[32 * j + l] >> 4;
+          if (qh) {
+            lo |= ((qh[l] >> (2 * j)) & 1) << 4;
+            hi |= ((qh[l] >> (2 * j + 1)) & 1) << 4;
+          }
+          o->q[64 * j + l] = (int16_t)lo;
+          o->q[64 * j + 32 + l] = (int16_t)hi;
         }
+      return 0;
+    }
+    case QREF_Q4_0:
+    case QREF_IQ4_NL: {
+      /* src/quants.h:136-148 (Q4_0: q = nibble - 8) and 527-538 (IQ4_NL: q = kvalues_iq4nl[nibble]): 8 blocks of
+       * (f16 d, 16 bytes: low nibbles = elements 0..15, high = 16..31) */
+      for (int b = 0; b < 8; ++b) {
+        const uint8_t* blk = p + 18 * b;
+        o->d8[b] = qref_fp16_to_f32(rd16(blk));
+        o->sc[b] = 1;
+        for (int i = 0; i < 16; ++i) {
+          const int lo = blk[2 + i] & 0xF, hi = blk[2 + i] >> 4;
+          o->q[32 * b + i] = (int16_t)(type == QREF_Q4_0 ? lo - 8 : k_iq4nl[lo]);
+          o->q[32 * b + 16 + i] = (int16_t)(type == QREF_Q4_0 ? hi - 8 : k_iq4nl[hi]);
+        }
+      }
       return 0;
     }
     case QREF_Q8_0: {
@@ -153,7 +182,7 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
       return 0;
     }
     case QREF_Q6_K: {
-      /* src/quants.h:125-141: ql[128] | qh[64] | scales[16] (int8, per 16) | d; q = (4 low bits | 2 high bits << 4)
+      /* src/quants.h:115-135: ql[128] | qh[64] | scales[16] (int8, per 16) | d; q = (4 low bits | 2 high bits << 4)
        * - 32, kept signed here (the reference keeps q and subtracts 32 in dequant_value, :320) */
       const uint8_t *ql = p, *qh = p + 128;
       o->d = qref_fp16_to_f32(rd16(p + 208));
@@ -183,8 +212,11 @@ int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
 /* src/quants.h:317-324 (dequant_value) via :496-555 (dequant_row): float expressions as written there */
 static float dequant_value(int type, const qref_sb* o, int e) {
   switch (type) {
-    case QREF_Q4_K: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - o->dmin * (float)o->mn[e / 32];
-    case QREF_Q8_0: return o->d8[e / 32] * (float)o->q[e];
+    case QREF_Q4_K:
+    case QREF_Q5_K: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - o->dmin * (float)o->mn[e / 32];
+    case QREF_Q8_0:
+    case QREF_Q4_0:
+    case QREF_IQ4_NL: return o->d8[e / 32] * (float)o->q[e];
     case QREF_Q6_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
     default: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - 0.0f;
   }
@@ -240,7 +272,7 @@ static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
     for (int i = 0; i < 16; ++i) r->sc[s * 16 + i] = o.sc16[i];
     for (int b = 0; b < 8; ++b) {
       r->mn[s * 8 + b] = o.mn[b];
-      r->d[s * 8 + b] = type == QREF_Q8_0 ? o.d8[b] : o.d;
+      r->d[s * 8 + b] = (type == QREF_Q8_0 || type == QREF_Q4_0 || type == QREF_IQ4_NL) ? o.d8[b] : o.d;
       r->dmin[s * 8 + b] = o.dmin;
     }
   }
@@ -259,7 +291,7 @@ static double row_dot(int type, const row_dec* r, int K, const int8_t* a, const 
     const int iv = r->sc[2 * b] * lo + r->sc[2 * b + 1] * hi;
     const float sa = asc[(size_t)b * M_stride + m];
     float v;
-    if (type == QREF_Q4_K) {
+    if (type == QREF_Q4_K || type == QREF_Q5_K) {
       const int bs = (int)absum[(size_t)(2 * b) * M_stride + m] + (int)absum[(size_t)(2 * b + 1) * M_stride + m];
       const int mv = r->mn[b] * bs;
       v = sa * (r->d[b] * (float)iv - r->dmin[b] * (float)mv);
@@ -373,7 +405,10 @@ int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_
   if (sbg < 0 || sbu < 0 || sbd < 0 || E % 256 || F % 256 || NU > 64 || T > M_stride) return -1;
   /* (types with per-block mins need the activation sums, which the expert path does not carry: the reference's
    *  expert GEMM takes no min types either, zero/engine_moe.h:284-289) */
-  if (type_gate == QREF_Q4_K || type_up == QREF_Q4_K || type_down == QREF_Q4_K) return -1;
+  if (type_gate == QREF_Q4_K || type_up == QREF_Q4_K || type_down == QREF_Q4_K || type_gate == QREF_Q5_K ||
+      type_up == QREF_Q5_K || type_down == QREF_Q5_K || type_gate == QREF_Q6_K || type_up == QREF_Q6_K ||
+      type_down == QREF_Q6_K)
+    return -1;
   int* ids = (int*)malloc(sizeof(int) * (size_t)T * NU);
   float* wts = (float*)malloc(sizeof(float) * (size_t)T * NU);
   qref_moe_route(logits, ldl, T, NE, NU, ids, wts, NULL);

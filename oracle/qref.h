@@ -18,7 +18,8 @@ extern "C" {
 #endif
 
 /* GGML type ids (src/gguf.h:20-27) */
-enum { QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q6_K = 14, QREF_IQ3_S = 21, QREF_IQ4_XS = 23 };
+enum { QREF_Q4_0 = 2, QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q5_K = 13, QREF_Q6_K = 14, QREF_IQ4_NL = 20, QREF_IQ3_S = 21,
+       QREF_IQ4_XS = 23 };
 
 /* A decoded 256-element superblock: integer quants plus the per-type scales.
  *   Q8_0:   w[e] = d8[e/32] * q[e]
@@ -26,6 +27,9 @@ enum { QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q6_K = 14, QREF_IQ3_S = 21, QREF_IQ4_
  *   IQ4_XS: w[e] = d * sc[e/32] * q[e]   (sc = ls - 32, q = kvalues_iq4nl[nibble])
  *   IQ3_S:  w[e] = d * sc[e/32] * q[e]   (sc = 1 + 2 * nibble, q = +-grid byte)
  *   Q6_K:   w[e] = d * sc16[e/16] * q[e]  (q = 6-bit value - 32; sc16 signed int8 per 16)
+ *   Q5_K:   as Q4_K with q = 0..31
+ *   Q4_0:   w[e] = d8[e/32] * q[e]        (q = nibble - 8)
+ *   IQ4_NL: w[e] = d8[e/32] * q[e]        (q = kvalues_iq4nl[nibble])
  * sc16[i] is the integer scale of elements 16i..16i+15 for every type (sc16[2b] = sc16[2b+1] = sc[b] except Q6_K). */
 typedef struct {
   float d, dmin;

@@ -79,3 +79,27 @@ def enc_q6_k(d, sc16, q):
                 ql[64 * n + l + 32 * (c & 1)] |= (v & 0xF) << (4 * (c >> 1))
                 qh[32 * n + l] |= ((v >> 4) & 3) << (2 * c)
     return np.concatenate([ql, qh, np.asarray(sc16, dtype=np.int8).view(np.uint8), _h(d)])
+
+
+def enc_q5_k(d, dmin, sc, mn, q):
+    """q: 256 ints 0..31 -> 176 bytes: d, dmin, scales[12] (as Q4_K), qh[32] (bit 2j / 2j+1 of qh[l]: fifth bit of
+    elements 64j + l / 64j + 32 + l), qs[128] (low nibbles as Q4_K)."""
+    base = enc_q4_k(d, dmin, sc, mn, np.asarray(q) & 0xF)
+    qh = np.zeros(32, dtype=np.uint8)
+    for j in range(4):
+        for l in range(32):
+            qh[l] |= ((int(q[64 * j + l]) >> 4) & 1) << (2 * j)
+            qh[l] |= ((int(q[64 * j + 32 + l]) >> 4) & 1) << (2 * j + 1)
+    return np.concatenate([base[:16], qh, base[16:]])
+
+
+def enc_q4_0(d8, nib):
+    """d8: 8 floats (one per 32), nib: 256 nibbles 0..15 (element order) -> 8 blocks of (f16 d, 16 bytes)."""
+    out = bytearray()
+    for b in range(8):
+        out += _h(d8[b]).tobytes()
+        out += bytes(int(nib[32 * b + i]) | (int(nib[32 * b + 16 + i]) << 4) for i in range(16))
+    return np.frombuffer(bytes(out), dtype=np.uint8)
+
+
+enc_iq4_nl = enc_q4_0  # (the same block struct: f16 d + 32 nibbles; the nibbles index the IQ4_NL codebook)

@@ -2,12 +2,13 @@
 
 Every expected value here is computed from the chosen integer FIELDS of each block (scales, nibbles, grid indices,
 sign bits) with numpy, following the GGML block definitions and the reference's per-element formulas
-(src/quants.h:149-158 Q8_0, 91-114 Q4_K, 125-141 Q6_K, 297-312 IQ4_XS, 240-262 IQ3_S; quantizer 559-576; GEMV per-block
-expression zero/kernels/decode.cl:695-706). Nothing here calls the oracle or the product, so the fixture pins both.
+(src/quants.h:149-158 Q8_0, 91-114 Q4_K / Q5_K, 115-135 Q6_K, 136-148 Q4_0 / IQ4_NL, 297-312 IQ4_XS, 240-262 IQ3_S;
+quantizer 559-576; GEMV per-block expression zero/kernels/decode.cl:695-706). Nothing here calls the oracle or the product, so the fixture pins both.
 The block bytes come from tests/encoders.py (packing written from the GGML structs).
 
 Edge cases: d = 0, d = +-65504 (largest half), d = 2^-24 (smallest subnormal half), all-15 nibbles, IQ3_S grid
-indices with bit 8 set, all sign bits set; quantizer rows with exact ties, zero blocks, +-amax, subnormals.
+indices with bit 8 set, all sign bits set, Q5_K with only the fifth bits set, all-0 and all-15 Q4_0 / IQ4_NL
+nibbles; quantizer rows with exact ties, zero blocks, +-amax, subnormals.
 
 Run: python tests/golden/make_golden.py   (deterministic; rewrites the .npz)
 """
@@ -59,6 +60,32 @@ def superblocks(qtype, rng, grid):
             e16 = np.arange(256) // 16
             dq = ((F32(d) * sc16[e16].astype(F32)) * (q6 - 32).astype(F32)).astype(F32)
             out.append((raw, q6 - 32, sc16, np.zeros(8, np.int64), F32(d), F32(0), dq))
+            continue
+        if qtype in (2, 20):  # Q4_0 / IQ4_NL: per-32 half scales, nibbles (q - 8 / the IQ4_NL codebook)
+            d8 = np.full(8, d, dtype=np.float16) if i < len(D_EDGE) else \
+                (np.abs(rng.standard_normal(8)) * 0.02 / 8).astype(np.float16)
+            nib = rng.integers(0, 16, 256)
+            if i == 1:
+                nib[:] = 15
+            if i == 2:
+                nib[:] = 0
+            raw = enc.enc_q4_0(d8.astype(np.float32), nib)
+            q = nib - 8 if qtype == 2 else KV[nib]
+            dq = (d8.astype(F32)[e] * q.astype(F32)).astype(F32)
+            out.append((raw, q, np.ones(8, np.int64), np.zeros(8, np.int64), d8.astype(F32), F32(0), dq))
+            continue
+        if qtype == 13:  # Q5_K: Q4_K's scales and mins, 5-bit q
+            dmin = np.float16(D_EDGE[(i + 1) % len(D_EDGE)]) if i < len(D_EDGE) else np.float16(abs(rng.standard_normal()) * 0.01)
+            sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+            q = rng.integers(0, 32, 256)
+            if i == 1:
+                q[:] = 31
+                sc[:] = 63
+            if i == 2:
+                q[:] = 16  # only the fifth bits set
+            raw = enc.enc_q5_k(d, dmin, sc, mn, q)
+            dq = ((F32(d) * sc[e].astype(F32)) * q.astype(F32) - F32(dmin) * mn[e].astype(F32)).astype(F32)
+            out.append((raw, q, sc, mn, F32(d), F32(dmin), dq))
             continue
         if qtype == 12:  # Q4_K
             dmin = np.float16(D_EDGE[(i + 1) % len(D_EDGE)]) if i < len(D_EDGE) else np.float16(abs(rng.standard_normal()) * 0.01)
@@ -134,7 +161,8 @@ def main():
     data.update(quant_x=x, quant_aq=aq, quant_asc=asc, quant_absum=absum)
     # per type: edge + random superblocks as an N x K matrix (N = 16 rows of K = 512), its dequantized values,
     # the int32 block sums against the first quantizer row pattern, and the GEMV output
-    for qtype, name in ((8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k")):
+    for qtype, name in ((8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k"), (13, "q5_k"),
+                        (2, "q4_0"), (20, "iq4_nl")):
         sbs = superblocks(qtype, rng, grid)
         N, K = 16, 512
         nsb = K // 256
@@ -159,9 +187,9 @@ def main():
                         iv = int(sc[j]) * int(np.dot(qq, a))
                     isum[n, b] = iv
                     sa = asc1[b, 0]
-                    if qtype == 8:
+                    if qtype in (8, 2, 20):
                         y[n] += float(sa * d[j] * F32(iv))
-                    elif qtype == 12:
+                    elif qtype in (12, 13):
                         mv = int(mn[j]) * int(a.sum())
                         msum[n, b] = mv
                         y[n] += float(sa * (d * F32(iv) - dmin * F32(mv)))

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(qm):
 def test_host_only_entry_points(qm):
     lib = qm.load_library()
     assert lib.qmatmul_sb_bytes(8) == 272 and lib.qmatmul_sb_bytes(12) == 144
-    assert lib.qmatmul_sb_bytes(21) == 110 and lib.qmatmul_sb_bytes(23) == 136 and lib.qmatmul_sb_bytes(2) == 0
+    assert lib.qmatmul_sb_bytes(21) == 110 and lib.qmatmul_sb_bytes(23) == 136 and lib.qmatmul_sb_bytes(6) == 0 and lib.qmatmul_sb_bytes(2) == 144
     assert lib.qmatmul_weight_bytes(23, 17408, 5120) >= 17408 * 20 * 136
     assert lib.qmatmul_weight_bytes(23, 16, 100) == 0
     assert lib.qmatmul_moe_workspace_size(4096, 256, 8, 2048, 512) > 32768 * 2048 * 4
@@ -48,7 +48,7 @@ def test_argument_errors_need_no_gpu(qm):
     assert lib.qmatmul_prepare_weight(23, None, 1, 16, 256, None, ctypes.byref(h)) == 1
     assert b"null" in lib.qmatmul_last_error()
     buf = (ctypes.c_uint8 * 16)()
-    assert lib.qmatmul_prepare_weight(2, buf, 0, 16, 256, None, ctypes.byref(h)) == 3
+    assert lib.qmatmul_prepare_weight(6, buf, 0, 16, 256, None, ctypes.byref(h)) == 3
     assert lib.qmatmul_prepare_weight(23, buf, 0, 16, 100, None, ctypes.byref(h)) == 2
     assert lib.qmatmul_gemv(None, None, None, None, 1, 1, None, 0, 0, 0, None) == 1
     assert lib.qmatmul_quantize_act(buf, 32, 1, 1, 33, buf, buf, buf, None) == 2

@@ -10,7 +10,8 @@ import pytest
 import oracle
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.npz")
-TYPES = [(8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k")]
+TYPES = [(8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k"), (13, "q5_k"), (2, "q4_0"),
+         (20, "iq4_nl")]
 K = 512
 
 
@@ -38,7 +39,7 @@ def test_oracle_blockdot_known_answers(g, qtype, name):
     aq, asc, absum = oracle.quantize_act(g[f"{name}_x"])
     C, isum, msum = oracle.blockdot(qtype, g[f"{name}_raw"], K, aq, asc, absum, blocksums=True)
     assert np.array_equal(isum[0].astype(np.int64), g[f"{name}_isum"])
-    if qtype == 12:
+    if qtype in (12, 13):
         assert np.array_equal(msum[0].astype(np.int64), g[f"{name}_msum"])
     y = g[f"{name}_y"]
     assert np.max(np.abs(C[0] - y)) <= 1e-6 * np.max(np.abs(y))
@@ -67,7 +68,7 @@ def test_gpu_gemv_known_answers(g, qm, dev, qtype, name):
     ygemm = qm.gemm(w, aq, asc, absum, M=16)
     torch.cuda.synchronize()
     assert np.array_equal(isum.cpu().numpy()[0].astype(np.int64), g[f"{name}_isum"])
-    if qtype == 12:
+    if qtype in (12, 13):
         assert np.array_equal(msum.cpu().numpy()[0].astype(np.int64), g[f"{name}_msum"])
     ref = g[f"{name}_y"]
     scale = np.max(np.abs(ref))

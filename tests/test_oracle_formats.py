@@ -131,7 +131,7 @@ def test_iq3_s_decoder_round_trip():
         assert np.array_equal(w, ref)
 
 
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
 def test_synth_weights_have_the_requested_statistics(qtype):
     W = F.synth_weight(qtype, 64, 512, seed=5)
     assert W.shape == (64, F.row_bytes(qtype, 512))
@@ -157,3 +157,36 @@ def test_q6_k_decoder_round_trip():
         w = oracle.dequant_rows(F.Q6_K, raw[None], 256)[0]
         ref = (np.float32(d) * sc16[np.arange(256) // 16].astype(np.float32) * (q - 32).astype(np.float32))
         assert np.array_equal(w, ref.astype(np.float32))
+
+
+def test_q5_k_decoder_round_trip():
+    rng = np.random.default_rng(6)
+    for it in range(40):
+        d, dmin = np.float16(rng.random()), np.float16(rng.random())
+        sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        q = rng.integers(0, 32, 256)
+        if it == 0:
+            q[:] = 31
+        raw = enc.enc_q5_k(d, dmin, sc, mn, q)
+        o = oracle.decode_sb(F.Q5_K, raw)
+        assert np.array_equal(o["q"], q) and np.array_equal(o["sc"], sc) and np.array_equal(o["mn"], mn)
+        w = oracle.dequant_rows(F.Q5_K, raw[None], 256)[0]
+        e = np.arange(256) // 32
+        ref = (np.float32(d) * sc[e].astype(np.float32) * q.astype(np.float32)
+               - np.float32(dmin) * mn[e].astype(np.float32)).astype(np.float32)
+        assert np.array_equal(w, ref)
+
+
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.IQ4_NL])
+def test_q4_0_and_iq4_nl_decoders(qtype):
+    rng = np.random.default_rng(qtype)
+    kv = _kv()
+    for _ in range(30):
+        d8 = (rng.standard_normal(8) * 0.1).astype(np.float16).astype(np.float32)
+        nib = rng.integers(0, 16, 256)
+        raw = enc.enc_q4_0(d8, nib)
+        o = oracle.decode_sb(qtype, raw)
+        q = nib - 8 if qtype == F.Q4_0 else kv[nib]
+        assert np.array_equal(o["q"], q) and np.array_equal(o["d8"], d8)
+        w = oracle.dequant_rows(qtype, raw[None], 256)[0]
+        assert np.array_equal(w, (np.repeat(d8, 32) * q.astype(np.float32)).astype(np.float32))

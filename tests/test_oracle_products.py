@@ -69,7 +69,7 @@ def test_quantize_layout_padding_and_absum():
 
 
 # ---- int8 block-dot products
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
 def test_blockdot_int_sums_brute_force(qtype):
     rng = np.random.default_rng(10 + qtype)
     N, K, M = 12, 512, 3
@@ -87,12 +87,12 @@ def test_blockdot_int_sums_brute_force(qtype):
             # per 16-element half: sc0 * lo + sc1 * hi (decode.cl:695-706)
             prod16 = (q * aq[m].astype(np.int64)).reshape(2 * nb, 16).sum(axis=1)
             assert np.array_equal(isum[m, n], (sc16 * prod16).reshape(nb, 2).sum(axis=1))
-            if qtype == F.Q4_K:
+            if qtype in (F.Q4_K, F.Q5_K):
                 bs = aq[m].astype(np.int64).reshape(nb, 32).sum(axis=1)
                 assert np.array_equal(msum[m, n], mn * bs)
 
 
-@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
 def test_blockdot_f32_vs_dequantized_double(qtype):
     rng = np.random.default_rng(20 + qtype)
     N, K, M = 40, 1024, 4
