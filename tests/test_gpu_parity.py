@@ -182,13 +182,14 @@ def test_gemm_f32_parity(qm, dev, qtype, M, Ms, N, K):
     assert rel_err(C.cpu().numpy(), oracle.matmul_f32(qtype, W, K, xq)) < TOL_F32_REF
 
 
-def test_gemm_accumulate_modes(qm, dev):
+@pytest.mark.parametrize("qtype", [F.IQ4_XS, F.Q4_K])
+def test_gemm_accumulate_modes(qm, dev, qtype):
     import torch
     M, N, K = 64, 256, 1024
-    W = F.synth_weight(F.IQ4_XS, N, K, seed=3)
+    W = F.synth_weight(qtype, N, K, seed=3)
     x = F.synth_activations(M, K, seed=4)
     aq, asc, absum = acts(qm, x, dev)
-    w = qm.QWeight(F.IQ4_XS, to_dev(W, dev), N, K)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
     base = qm.gemm(w, aq, asc, absum)
     C = torch.randn(M, 2 * N + 16, device=dev)
     C0 = C.clone()
