@@ -12,7 +12,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqmatmul.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HOST_SOURCES = ["qm_gguf.cpp"]  # host-only C++ (g++)
-SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemm.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
+SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemv_q8.hip", "qm_gemv_k.hip", "qm_gemv_q6.hip", "qm_gemv_iq.hip", "qm_gemm.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt",
@@ -30,8 +30,19 @@ def _compile_host(src):
     return obj
 
 
-def _compile(src):
+def _stale(src, obj):
+    """True when obj is missing or older than src or any header in csrc/."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".h", ".inc"))]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile(src, incremental=False):
     obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [HIPCC, *FLAGS, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # (hipcc's host pass does not know the packed-fp32 feature name; that warning is expected)
@@ -43,10 +54,11 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
+def build(verbose=True, incremental=False):
+    """Compiles every source (incremental=True: only those whose object is older than the source or a header)."""
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES)) + list(ex.map(_compile_host, HOST_SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, incremental), SOURCES)) + list(ex.map(_compile_host, HOST_SOURCES))
     tmp = LIB + ".tmp"
     r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs],
                        capture_output=True, text=True)
@@ -59,4 +71,4 @@ def build(verbose=True):
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv)

@@ -1,417 +1,20 @@
-// Decode GEMV on the prepared planes: C[t][n] (+)= sum_k W[n][k] * a_t[k] for T <= 8 tokens per weight read.
-//
-// Mapping: a wave is split into 64/LPR lane groups; each group owns R consecutive rows and walks the row's 32-blocks
-// with its LPR lanes (lane j: blocks j, j + LPR, ...). Per block a lane loads the token activations once (32 int8 +
-// the f32 scale per token) and, per row, the block's payload (one 16-byte load for the 4-bit types) and header,
-// decodes 32 int8 weights in registers (IQ4_XS: byte permutes over the 16-value codebook; IQ3_S: grid and sign
-// masks from LDS), takes 8 v_dot4_i32_i8 per token and scales the int32 block sum in f32 -- per block exactly
-// the reference's expression `sa * d * (float)(sc0 * lo + sc1 * hi)` (zero/kernels/decode.cl:695-706, 1107-1115),
-// with the min term for Q4_K. A cross-lane butterfly then sums the group's partial results.
-#include <stdlib.h>
-
-#include "qm_decode.h"
+// Decode GEMV entry: routes a weight type to its instantiation (qm_gemv_*.hip; kernels in qm_gemv_impl.h).
+#include "qm_launch.h"
 
 namespace qm {
 
-// U consecutive iterations of the block loop are loaded before any is decoded, so each lane keeps U*R weight loads
-// in flight (the loop is bandwidth-bound: bytes in flight, not instructions, set its speed).
-template <int TYPE, int LPR, int R, int TB, int U, bool DUMP>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  __shared__ typename LdsFor<TYPE>::type lds;
-  if constexpr (TYPE == T_IQ3_S) {
-    iq3_lds_fill(&lds);
-    __syncthreads();
-  }
-  constexpr int G = 64 / LPR;
-  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane / LPR, gl = lane % LPR;
-  const int row0 = ((blockIdx.x * 4 + wave) * G + grp) * R;
-  const int T = a.T;
-  const KvTab kv = kv_tab();
-
-  float acc[R][TB];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int t = 0; t < TB; ++t) acc[r][t] = 0.0f;
-
-  for (int b0 = gl; b0 < nb; b0 += LPR * U) {
-    RawBlk raw[U][R];
-    uint32_t av[U][TB][8];
-    float sa[U][TB];
-    int bs0[U][TB], bs1[U][TB];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = min(b0 + LPR * u, nb - 1);  // (past the row's end: reload its last block, masked below)
-#pragma unroll
-      for (int r = 0; r < R; ++r) raw[u][r] = load_block<TYPE>(a.w, min(row0 + r, rows - 1), b);
-#pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        const int tt = min(t, T - 1);
-        const uint4* ap = (const uint4*)(a.aq + (size_t)tt * K + 32 * b);
-        const uint4 x0 = ap[0], x1 = ap[1];
-        av[u][t][0] = x0.x; av[u][t][1] = x0.y; av[u][t][2] = x0.z; av[u][t][3] = x0.w;
-        av[u][t][4] = x1.x; av[u][t][5] = x1.y; av[u][t][6] = x1.z; av[u][t][7] = x1.w;
-        sa[u][t] = DUMP ? 0.0f : a.asc[(size_t)b * a.M_stride + tt];
-        if constexpr (kNeedsBsum<TYPE>) {
-          bs0[u][t] = a.absum[(size_t)(2 * b) * a.M_stride + tt];
-          bs1[u][t] = a.absum[(size_t)(2 * b + 1) * a.M_stride + tt];
-        } else {
-          bs0[u][t] = bs1[u][t] = 0;
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = b0 + LPR * u;
-      const bool live = b < nb;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        uint32_t wd[8];
-        int sc, sc1, mn;
-        BlockInts bi;
-        decode_block32<TYPE>(raw[u][r], &lds, b & 7, kv, wd, sc, sc1, mn, bi.d, bi.dmin);
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          const uint4 x0 = make_uint4(av[u][t][0], av[u][t][1], av[u][t][2], av[u][t][3]);
-          const uint4 x1 = make_uint4(av[u][t][4], av[u][t][5], av[u][t][6], av[u][t][7]);
-          block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, bs0[u][t], bs1[u][t], bi.iv, bi.mv);
-          if constexpr (DUMP) {
-            if (live && t < T && row0 + r < rows) {
-              const size_t o = ((size_t)t * rows + (row0 + r)) * nb + b;
-              a.dbg_isum[o] = bi.iv;
-              if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = bi.mv;
-            }
-          } else if (live) {
-            acc[r][t] += block_value<TYPE>(sa[u][t], bi);
-          }
-        }
-      }
-    }
-  }
-  if constexpr (!DUMP) {
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        const float v = wave_sum_width(acc[r][t], LPR);
-        const int n = row0 + r;
-        if (gl == 0 && n < rows && t < T) {
-          float* cp = a.C + (size_t)t * a.ldc + a.c_off + n;
-          *cp = a.accumulate ? *cp + v : v;
-        }
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Batch-1 decode GEMV (the token-generation case). The token's int8 row, its per-32 scales (and, for Q4_K, per-32
-// sums) are staged in LDS once per work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each
-// 32-block) so 32 lanes reading consecutive blocks read consecutive 16-byte words. A 32-lane group owns one row at a
-// time: lane j takes blocks j, j + 32, ... of the row, CH of them per step, and the next step's weight loads (next
-// chunk or next row) are issued before the current step is decoded, so every lane keeps 2*CH 16-byte streaming loads
-// in flight. Each group walks `rpg` rows spaced 8 apart (the work-group's 8 groups interleave rows). Requires K/32 to
-// be a multiple of 32.
-template <int TYPE, int CH, bool EXACT>
-__global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
-  extern __shared__ uint4 smem[];
-  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
-  uint8_t* sq = (uint8_t*)smem;            // [2][nb][16] int8 planes
-  float* ssc = (float*)(sq + (size_t)K);    // [nb] scales
-  int* sbs = (int*)(ssc + nb);              // [nb] per-16 sums of each block, packed int16 pairs (Q4_K, Q6_K)
-  const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
-  const int nch = (nb / 32 + CH - 1) / CH;  // steps per row
-  const int row_base = blockIdx.x * 8 * rpg + grp;
-  const int steps = rpg * nch;
-
-  RawBlk cur[CH], nxt[CH];
-  using Tr = Traits<TYPE>;
-  auto fetch = [&](int step, RawBlk* dst) {
-    const int i = step / nch, c = step % nch;
-    const int n = min(row_base + 8 * i, rows - 1);
-    const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
-    const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + 32 * (c * CH + u);
-      dst[u] = load_block_at<TYPE>(qrow, hrow, EXACT ? b : min(b, nb - 1));
-    }
-  };
-  fetch(0, cur);
-  // (the first weight loads are in flight while the activations are staged)
-  __shared__ typename LdsFor<TYPE>::type lds;
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
-  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
-    const int b = i >> 1, h = i & 1;
-    *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
-  }
-  for (int b = threadIdx.x; b < nb; b += 256) {
-    ssc[b] = a.asc[(size_t)b * a.M_stride];
-    if constexpr (kNeedsBsum<TYPE>)
-      sbs[b] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride] | ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride] << 16);
-  }
-  __syncthreads();
-
-  const KvTab kv = kv_tab();
-  float acc = 0.0f;
-  for (int step = 0; step < steps; ++step) {
-    if (step + 1 < steps) fetch(step + 1, nxt);
-    const int i = step / nch, c = step % nch;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + 32 * (c * CH + u);
-      if (EXACT || b < nb) {
-        const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
-        const int bp = kNeedsBsum<TYPE> ? sbs[b] : 0;
-        const BlockInts bi = block_product<TYPE>(cur[u], &lds, b & 7, kv, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16);
-        acc += block_value<TYPE>(ssc[b], bi);
-      }
-    }
-    if (c == nch - 1) {
-      const float v = wave_sum_width(acc, 32);
-      const int n = row_base + 8 * i;
-      if (gl == 0 && n < rows) {
-        float* cp = a.C + a.c_off + n;
-        *cp = a.accumulate ? *cp + v : v;
-      }
-      acc = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < CH; ++u) cur[u] = nxt[u];
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Batch-1 decode GEMV, persistent sweep. LPR lanes share a row (32, or 128 = two waves with an LDS combine); lane j
-// takes blocks j, j + LPR, ... (CH of them). The grid is a few work-groups per CU and lane group g walks rows
-// g, g + G, g + 2G, ... (G = lane groups in the grid), so the whole grid moves through the weight matrix together
-// and every group has one row in flight: it decodes the row once its loads land and only then issues the next row's
-// loads. Measured on MI355X this beats both issuing every row's loads up front (the decode then piles up behind the
-// stream) and keeping two rows in flight per group. The token's activations are staged in LDS once per work-group, as in gemv1_kernel.
-template <int TYPE, int LPR, int CH, bool EXACT, int TB>
-__global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
-  extern __shared__ uint4 smem[];
-  using Tr = Traits<TYPE>;
-  constexpr int GPW = 256 / LPR;                 // lane groups per work-group
-  constexpr int WPR = LPR > 64 ? LPR / 64 : 1;   // waves per row
-  const int K = a.w.K, nb = K / 32, rows = a.w.rows, T = a.T;
-  // LDS: per token t < TB: int8 planes [2][nb][16] at t*K, then scales [TB][nb], then Q4_K block sums [TB][nb]
-  uint8_t* sq = (uint8_t*)smem;
-  float* ssc = (float*)(sq + (size_t)TB * K);
-  int* sbs = (int*)(ssc + (size_t)TB * nb);
-  __shared__ typename LdsFor<TYPE>::type lds;
-  __shared__ float part[2][GPW][WPR][TB];
-  const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
-  const int G = gridDim.x * GPW;
-  const int g0 = blockIdx.x * GPW + grp;
-  // steps: the group's rows; with two waves per row every group of the work-group runs the same number of steps
-  // (the combine's barrier), the extra steps of the shorter groups recomputing the last row without storing it
-  const int steps = WPR == 1 ? (g0 < rows ? (rows - 1 - g0) / G + 1 : 0) : (rows - 1 - (int)blockIdx.x * GPW) / G + 1;
-  RawBlk cur[CH];
-  auto fetch = [&](int i, RawBlk* dst) {
-    const int n = min(g0 + G * i, rows - 1);
-    const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
-    const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + LPR * u;
-      dst[u] = load_block_at<TYPE>(qrow, hrow, EXACT ? b : min(b, nb - 1));
-    }
-  };
-  fetch(0, cur);
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
-  for (int i = threadIdx.x; i < 2 * nb * TB; i += 256) {
-    const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
-    const int tt = min(t, T - 1);  // (tokens past T: a copy of the last, never stored)
-    *(uint4*)(sq + (size_t)t * K + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + (size_t)tt * K + 32 * b + 16 * h);
-  }
-  for (int i = threadIdx.x; i < nb * TB; i += 256) {
-    const int t = i / nb, b = i % nb, tt = min(t, T - 1);
-    ssc[i] = a.asc[(size_t)b * a.M_stride + tt];
-    if constexpr (kNeedsBsum<TYPE>)
-      sbs[i] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride + tt] |
-               ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt] << 16);
-  }
-  __syncthreads();
-  const KvTab kv = kv_tab();
-  for (int i = 0; i < steps; ++i) {
-    float acc[TB];
-#pragma unroll
-    for (int t = 0; t < TB; ++t) acc[t] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + LPR * u;
-      if (EXACT || b < nb) {
-        uint32_t wd[8];
-        int sc, sc1, mn;
-        BlockInts bi;
-        decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, sc1, mn, bi.d, bi.dmin);
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          const uint8_t* st = sq + (size_t)t * K;
-          const uint4 x0 = *(const uint4*)(st + b * 16), x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
-          const int bp = kNeedsBsum<TYPE> ? sbs[t * nb + b] : 0;
-          block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16, bi.iv, bi.mv);
-          acc[t] += block_value<TYPE>(ssc[t * nb + b], bi);
-        }
-      }
-    }
-    fetch(i + 1, cur);  // (unconditional and clamped to the last row: no branch between the decode and the loads)
-    const int n = g0 + G * i;
-    float v[TB];
-    if constexpr (WPR == 1) {
-#pragma unroll
-      for (int t = 0; t < TB; ++t) v[t] = wave_sum_width(acc[t], LPR);
-    } else {
-#pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        const float w = wave_sum_width(acc[t], 64);
-        if ((threadIdx.x & 63) == 0) part[i & 1][grp][gl >> 6][t] = w;
-      }
-      __syncthreads();  // (double-buffered by step parity: one barrier per step)
-#pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        v[t] = part[i & 1][grp][0][t];
-#pragma unroll
-        for (int k = 1; k < WPR; ++k) v[t] += part[i & 1][grp][k][t];
-      }
-    }
-    if (gl == 0 && n < rows) {
-#pragma unroll
-      for (int t = 0; t < TB; ++t)
-        if (t < T) {
-          float* cp = a.C + (size_t)t * a.ldc + a.c_off + n;
-          *cp = a.accumulate ? *cp + v[t] : v[t];
-        }
-    }
-  }
-}
-
-// LDS bytes of gemvs_kernel for TB tokens
-static size_t gemvs_lds(int type, int K, int TB) {
-  const int nb = K / 32;
-  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
-}
-
-template <int TYPE, int LPR, int CH, bool EXACT, int TB>
-static hipError_t gos(const GemvArgs& a, hipStream_t s) {
-  constexpr int GPW = 256 / LPR;
-  // two work-groups per CU (256 CUs), fewer when the matrix has fewer rows than lane groups
-  const int wgs = min(512, (a.w.rows + GPW - 1) / GPW);
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
-  return hipGetLastError();
-}
-
-template <int TYPE, int LPR, int CH, bool EXACT>
-static hipError_t gos_tb(const GemvArgs& a, hipStream_t s) {
-  switch (a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8) {
-    case 1: return gos<TYPE, LPR, CH, EXACT, 1>(a, s);
-    case 2: return gos<TYPE, LPR, CH, EXACT, 2>(a, s);
-    case 4: return gos<TYPE, LPR, CH, EXACT, 4>(a, s);
-    default: return gos<TYPE, LPR, CH, EXACT, 8>(a, s);
-  }
-}
-
-template <int TYPE, int CH, bool EXACT>
-static hipError_t go1(const GemvArgs& a, hipStream_t s) {
-  const int nb = a.w.K / 32;
-  // rows per 32-lane group: enough work-groups to fill 256 CUs twice, each group walking several rows
-  const int rows = a.w.rows;
-  int rpg = 1;
-  while (rpg < 16 && (rows + 8 * rpg * 2 - 1) / (8 * rpg * 2) >= 1024) rpg *= 2;
-  const unsigned grid = (unsigned)((rows + 8 * rpg - 1) / (8 * rpg));
-  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (kNeedsBsum<TYPE> ? sizeof(int) * nb : 0);
-  gemv1_kernel<TYPE, CH, EXACT><<<grid, 256, shm, s>>>(a, rpg);
-  return hipGetLastError();
-}
-
-template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
-static hipError_t go(const GemvArgs& a, hipStream_t s) {
-  constexpr int rows_per_wg = 4 * (64 / LPR) * R;
-  const dim3 grid((unsigned)((a.w.rows + rows_per_wg - 1) / rows_per_wg)), block(256);
-  gemv_kernel<TYPE, LPR, R, TB, U, DUMP><<<grid, block, 0, s>>>(a);
-  return hipGetLastError();
-}
-
-template <int TYPE>
-static hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
-  const int nb = a.w.K / 32;
-  if (a.dbg_isum) {
-    switch (a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8) {
-      case 1: return go<TYPE, 8, 1, 1, true>(a, s);
-      case 2: return go<TYPE, 8, 1, 2, true>(a, s);
-      case 4: return go<TYPE, 8, 1, 4, true>(a, s);
-      default: return go<TYPE, 8, 1, 8, true>(a, s);
-    }
-  }
-  const bool l32 = nb % 32 == 0;
-  static const int sweep = getenv("QM_GEMV_SWEEP") ? atoi(getenv("QM_GEMV_SWEEP")) : 1;
-  if (sweep && nb <= 1024) {
-    // tokens per launch: as many as fit in 80 KB of LDS (two work-groups per CU), up to 8; more tokens -> chunks
-    // of tokens, each launch reading the weights once
-    int tb = 8;
-    while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > 80 * 1024) tb >>= 1;
-    if (gemvs_lds(TYPE, a.w.K, tb) <= 80 * 1024) {
-      for (int t0 = 0; t0 < a.T; t0 += tb) {
-        GemvArgs c = a;
-        c.T = min(tb, a.T - t0);
-        c.aq = a.aq + (size_t)t0 * a.w.K;
-        c.asc = a.asc + t0;
-        c.absum = a.absum + t0;
-        c.C = a.C + (size_t)t0 * a.ldc;
-        hipError_t e;
-        if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
-          switch ((nb + 31) / 32) {
-            case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true>(c, s) : gos_tb<TYPE, 32, 1, false>(c, s); break;
-            case 2: e = nb == 64 ? gos_tb<TYPE, 32, 2, true>(c, s) : gos_tb<TYPE, 32, 2, false>(c, s); break;
-            case 3: e = nb == 96 ? gos_tb<TYPE, 32, 3, true>(c, s) : gos_tb<TYPE, 32, 3, false>(c, s); break;
-            case 4: e = nb == 128 ? gos_tb<TYPE, 32, 4, true>(c, s) : gos_tb<TYPE, 32, 4, false>(c, s); break;
-            case 5: e = nb == 160 ? gos_tb<TYPE, 32, 5, true>(c, s) : gos_tb<TYPE, 32, 5, false>(c, s); break;
-            case 6: e = nb == 192 ? gos_tb<TYPE, 32, 6, true>(c, s) : gos_tb<TYPE, 32, 6, false>(c, s); break;
-            case 7: e = nb == 224 ? gos_tb<TYPE, 32, 7, true>(c, s) : gos_tb<TYPE, 32, 7, false>(c, s); break;
-            default: e = nb == 256 ? gos_tb<TYPE, 32, 8, true>(c, s) : gos_tb<TYPE, 32, 8, false>(c, s); break;
-          }
-        } else {  // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
-          switch ((nb + 127) / 128) {
-            case 3: e = nb == 384 ? gos_tb<TYPE, 128, 3, true>(c, s) : gos_tb<TYPE, 128, 3, false>(c, s); break;
-            case 4: e = nb == 512 ? gos_tb<TYPE, 128, 4, true>(c, s) : gos_tb<TYPE, 128, 4, false>(c, s); break;
-            case 5: e = nb == 640 ? gos_tb<TYPE, 128, 5, true>(c, s) : gos_tb<TYPE, 128, 5, false>(c, s); break;
-            case 6: e = nb == 768 ? gos_tb<TYPE, 128, 6, true>(c, s) : gos_tb<TYPE, 128, 6, false>(c, s); break;
-            case 7: e = nb == 896 ? gos_tb<TYPE, 128, 7, true>(c, s) : gos_tb<TYPE, 128, 7, false>(c, s); break;
-            default: e = nb == 1024 ? gos_tb<TYPE, 128, 8, true>(c, s) : gos_tb<TYPE, 128, 8, false>(c, s); break;
-          }
-        }
-        if (e != hipSuccess) return e;
-      }
-      return hipSuccess;
-    }
-  }
-  if (a.T <= 1 && l32 && a.w.K <= 32768) {
-    const int per_lane = nb / 32;  // blocks per lane per row
-    if (per_lane % 5 == 0) return go1<TYPE, 5, true>(a, s);
-    if (per_lane % 4 == 0) return go1<TYPE, 4, true>(a, s);
-    return go1<TYPE, 6, false>(a, s);
-  }
-  if (a.T <= 1) {
-    // short rows (many rows): 2 rows per lane group; long rows (few rows, K >= 8192): 1, for more waves in flight
-    if (l32) return a.w.K >= 8192 ? go<TYPE, 32, 1, 1, false>(a, s) : go<TYPE, 32, 2, 1, false>(a, s);
-    return go<TYPE, 8, 2, 1, false>(a, s);
-  }
-  if (a.T <= 2) return l32 ? go<TYPE, 32, 1, 2, false>(a, s) : go<TYPE, 8, 1, 2, false>(a, s);
-  if (a.T <= 4) return l32 ? go<TYPE, 32, 1, 4, false>(a, s) : go<TYPE, 8, 1, 4, false>(a, s);
-  return l32 ? go<TYPE, 32, 1, 8, false>(a, s) : go<TYPE, 8, 1, 8, false>(a, s);
-}
+template <int TYPE> hipError_t gemv_dispatch(const GemvArgs& a, hipStream_t s);
 
 hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
   switch (type) {
-    case T_Q8_0: return dispatch<T_Q8_0>(a, s);
-    case T_Q4_K: return dispatch<T_Q4_K>(a, s);
-    case T_IQ4_XS: return dispatch<T_IQ4_XS>(a, s);
-    case T_IQ3_S: return dispatch<T_IQ3_S>(a, s);
-    case T_Q6_K: return dispatch<T_Q6_K>(a, s);
-    case T_Q5_K: return dispatch<T_Q5_K>(a, s);
-    case T_Q4_0: return dispatch<T_Q4_0>(a, s);
-    case T_IQ4_NL: return dispatch<T_IQ4_NL>(a, s);
+    case T_Q8_0: return gemv_dispatch<T_Q8_0>(a, s);
+    case T_Q4_K: return gemv_dispatch<T_Q4_K>(a, s);
+    case T_IQ4_XS: return gemv_dispatch<T_IQ4_XS>(a, s);
+    case T_IQ3_S: return gemv_dispatch<T_IQ3_S>(a, s);
+    case T_Q6_K: return gemv_dispatch<T_Q6_K>(a, s);
+    case T_Q5_K: return gemv_dispatch<T_Q5_K>(a, s);
+    case T_Q4_0: return gemv_dispatch<T_Q4_0>(a, s);
+    case T_IQ4_NL: return gemv_dispatch<T_IQ4_NL>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

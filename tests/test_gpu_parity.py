@@ -236,3 +236,28 @@ def test_iq3_s_baseline_5120(qm, dev, M):
     ref = oracle.blockdot(F.IQ3_S, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=M,
                           col_stride=stride)
     assert rel_err(C.cpu().numpy()[:, ::stride], ref[:, ::stride]) < TOL_INT8_PATH
+
+
+@pytest.mark.parametrize("M,N,K,c_off,extra", [(300, 144, 1024, 3, 5), (64, 128, 256, 0, 0), (257, 272, 2048, 1, 2)])
+def test_gemm_q4_k_edges(qm, dev, M, N, K, c_off, extra):
+    """Q4_K prompt GEMM at ragged shapes (token and row tiles partly filled, unaligned output columns) with
+    superblocks whose d or dmin is zero (the carried-scale path treats d = 0 specially)."""
+    import torch
+    W = F.synth_weight(F.Q4_K, N, K, seed=M + N).copy()
+    nsb = K // 256
+    sbv = W.reshape(N, nsb, 144)
+    sbv[::3, 0, 0:2] = 0      # d = 0 in the first superblock of every third row
+    sbv[1::5, -1, 2:4] = 0    # dmin = 0 in the last superblock of every fifth row
+    sbv[2, :, 0:4] = 0        # row 2: d = dmin = 0 everywhere
+    x = F.synth_activations(M, K, seed=M, outlier_frac=0.01, outlier_scale=20.0)
+    aq, asc, absum = acts(qm, x, dev)
+    w = qm.QWeight(F.Q4_K, to_dev(W, dev), N, K)
+    ldc = c_off + N + extra
+    C = torch.full((M, ldc), 7.0, device=dev)
+    qm.gemm(w, aq, asc, absum, C=C, ldc=ldc, c_off=c_off)
+    torch.cuda.synchronize()
+    Cn = C.cpu().numpy()
+    ref = oracle.blockdot(F.Q4_K, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=M)
+    assert rel_err(Cn[:, c_off:c_off + N], ref) < TOL_INT8_PATH
+    assert np.all(Cn[:, :c_off] == 7.0) and np.all(Cn[:, c_off + N:] == 7.0)
+    assert np.all(Cn[:, c_off + 2] == 0.0)  # row 2 of the weight is all zero
