@@ -1,18 +1,21 @@
 """GGUF block geometry of the weight types of the path, and seeded synthetic weights in GGUF block form.
 
 Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144,
-Q5_K 256 / 176, Q6_K 256 / 210, IQ3_S 256 / 110, IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
+Q5_K 256 / 176, Q6_K 256 / 210, IQ2_XXS 256 / 66, IQ2_XS 256 / 74, IQ2_S 256 / 82, IQ3_XXS 256 / 98, IQ3_S 256 / 110,
+IQ4_XS 256 / 136). The synthetic generators produce the BASELINE configurations' distributions directly as block
 bytes: every quant / index / sign / sub-scale bit uniform, the f16 super-scales |N(0, sigma)|.
 """
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS = 2, 8, 12, 13, 14, 20, 21, 23
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ2_S = 16, 17, 18, 22
 TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S",
-              IQ4_XS: "IQ4_XS"}
+              IQ4_XS: "IQ4_XS", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ3_XXS: "IQ3_XXS", IQ2_S: "IQ2_S"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 # bytes of one 256-element superblock (Q8_0: 8 blocks of 34)
-SB_BYTES = {Q4_0: 144, Q8_0: 272, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 144, IQ3_S: 110, IQ4_XS: 136}
+SB_BYTES = {Q4_0: 144, Q8_0: 272, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 144, IQ3_S: 110, IQ4_XS: 136, IQ2_XXS: 66,
+            IQ2_XS: 74, IQ3_XXS: 98, IQ2_S: 82}
 
 
 def row_bytes(qtype, K):
@@ -41,6 +44,8 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     Q6_K:   6-bit quants and int8 per-16 scales uniform, d = f16(|N(0, 0.01)|) (d is the last field)
     Q5_K:   as Q4_K (the fifth bits uniform too)
     Q4_0 / IQ4_NL: nibbles uniform, d = f16(|N(0, 0.02)| / 8) per 32
+    IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS: grid indices, sign indices or bits and 4-bit sub-scales uniform,
+            d = f16(|N(0, 0.01)|)
     """
     rng = np.random.default_rng(seed)
     nsb = K // 256

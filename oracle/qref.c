@@ -14,6 +14,11 @@
 
 static const uint32_t k_iq3s_grid[512] = QM_IQ3S_GRID_INIT;
 static const int8_t k_iq4nl[16] = QM_IQ4NL_VALUES_INIT;
+static const uint64_t k_iq2xxs_grid[256] = QM_IQ2XXS_GRID_INIT;
+static const uint64_t k_iq2xs_grid[512] = QM_IQ2XS_GRID_INIT;
+static const uint64_t k_iq2s_grid[1024] = QM_IQ2S_GRID_INIT;
+static const uint32_t k_iq3xxs_grid[256] = QM_IQ3XXS_GRID_INIT;
+static const uint8_t k_ksigns[128] = QM_KSIGNS_IQ2XS_INIT;
 
 /* src/quants.h:17-31 -- IEEE half to float, subnormals normalised by shifting */
 float qref_fp16_to_f32(uint16_t h) {
@@ -74,6 +79,10 @@ int qref_block_info(int type, int* blk, int* bytes) {
     case QREF_IQ4_NL: *blk = 32; *bytes = 18; return 0;
     case QREF_IQ3_S: *blk = 256; *bytes = 110; return 0;
     case QREF_IQ4_XS: *blk = 256; *bytes = 136; return 0;
+    case QREF_IQ2_XXS: *blk = 256; *bytes = 66; return 0;
+    case QREF_IQ2_XS: *blk = 256; *bytes = 74; return 0;
+    case QREF_IQ2_S: *blk = 256; *bytes = 82; return 0;
+    case QREF_IQ3_XXS: *blk = 256; *bytes = 98; return 0;
     default: return -1;
   }
 }
@@ -85,6 +94,15 @@ int qref_sb_bytes(int type) {
 }
 
 static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static uint32_t rd32(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
+
+/* 8 elements from an 8-byte grid entry and a sign byte (bit j set: element j negative) (src/quants.h:178-180) */
+static void grid8_signs(uint64_t g, unsigned sg, int16_t* q) {
+  for (int j = 0; j < 8; ++j) {
+    const int v = (int)((g >> (8 * j)) & 0xFF);
+    q[j] = (int16_t)((sg & (1u << j)) ? -v : v);
+  }
+}
 
 /* src/quants.h:61-69 */
 static void scale_min_k4(int j, const uint8_t* q, int* d, int* m) {
@@ -97,8 +115,9 @@ static void scale_min_k4(int j, const uint8_t* q, int* d, int* m) {
   }
 }
 
-/* src/quants.h:89-315 (cases Q4_K / Q5_K 91-114, Q6_K 115-135, Q4_0 136-148, Q8_0 149-158, IQ3_S 240-262,
- * IQ4_XS 297-312; IQ4_NL from dequant_row 527-538) */
+/* src/quants.h:89-315 (cases Q4_K / Q5_K 91-114, Q6_K 115-135, Q4_0 136-148, Q8_0 149-158, IQ2_XXS 170-184,
+ * IQ2_XS 185-201, IQ2_S 202-219, IQ3_XXS 220-239, IQ3_S 240-262, IQ4_XS 297-312; IQ4_NL from dequant_row
+ * 527-538) */
 static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
   memset(o, 0, sizeof(*o));
   switch (type) {
@@ -167,6 +186,68 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
       }
       return 0;
     }
+    case QREF_IQ2_XXS: {
+      /* src/quants.h:170-184: d (f16) then 8 blocks of (a0: 4 grid indices, a1: 4 x 7-bit sign indices + 4-bit
+       * scale); wd = d / 8 */
+      o->d = qref_fp16_to_f32(rd16(p)) / 8;
+      for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t a0 = rd32(p + 2 + 8 * ib), a1 = rd32(p + 2 + 8 * ib + 4);
+        o->sc[ib] = 1 + 2 * (int)(a1 >> 28);
+        for (int l = 0; l < 4; ++l)
+          grid8_signs(k_iq2xxs_grid[(a0 >> (8 * l)) & 0xFF], k_ksigns[(a1 >> (7 * l)) & 127], o->q + 32 * ib + 8 * l);
+      }
+      return 0;
+    }
+    case QREF_IQ2_XS: {
+      /* src/quants.h:185-201: d, qs[32] (u16: 9-bit grid index, 7-bit sign index), scales[8] (4 bits per 16) */
+      o->d = qref_fp16_to_f32(rd16(p)) / 8;
+      const uint8_t* scales = p + 66;
+      for (int ib = 0; ib < 8; ++ib) {
+        o->sc16[2 * ib] = 1 + 2 * (scales[ib] & 0xF);
+        o->sc16[2 * ib + 1] = 1 + 2 * (scales[ib] >> 4);
+        o->sc[ib] = o->sc16[2 * ib];
+        for (int l = 0; l < 4; ++l) {
+          const unsigned q16 = rd16(p + 2 + 2 * (4 * ib + l));
+          grid8_signs(k_iq2xs_grid[q16 & 511], k_ksigns[q16 >> 9], o->q + 32 * ib + 8 * l);
+        }
+      }
+      return 0;
+    }
+    case QREF_IQ2_S: {
+      /* src/quants.h:202-219: d, qs[32] (grid index low 8 bits), signs[32], qh[8] (2 high bits per 8 elements),
+       * scales[8] (4 bits per 16) */
+      o->d = qref_fp16_to_f32(rd16(p)) / 8;
+      const uint8_t *qs = p + 2, *signs = p + 34, *qh = p + 66, *scales = p + 74;
+      for (int ib = 0; ib < 8; ++ib) {
+        o->sc16[2 * ib] = 1 + 2 * (scales[ib] & 0xF);
+        o->sc16[2 * ib + 1] = 1 + 2 * (scales[ib] >> 4);
+        o->sc[ib] = o->sc16[2 * ib];
+        for (int l = 0; l < 4; ++l)
+          grid8_signs(k_iq2s_grid[qs[4 * ib + l] | ((qh[ib] << (8 - 2 * l)) & 0x300)], signs[4 * ib + l],
+                      o->q + 32 * ib + 8 * l);
+      }
+      return 0;
+    }
+    case QREF_IQ3_XXS: {
+      /* src/quants.h:220-239: d, qs[64] (grid indices), then per block a word of 4 x 7-bit sign indices + 4-bit
+       * scale; wd = d / 4 */
+      o->d = qref_fp16_to_f32(rd16(p)) / 4;
+      const uint8_t *qs = p + 2, *ss = p + 66;
+      for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t a = rd32(ss + 4 * ib);
+        o->sc[ib] = 1 + 2 * (int)(a >> 28);
+        for (int l = 0; l < 4; ++l) {
+          const unsigned sg = k_ksigns[(a >> (7 * l)) & 127];
+          const uint32_t g1 = k_iq3xxs_grid[qs[8 * ib + 2 * l]], g2 = k_iq3xxs_grid[qs[8 * ib + 2 * l + 1]];
+          for (int j = 0; j < 4; ++j) {
+            const int v1 = (int)((g1 >> (8 * j)) & 0xFF), v2 = (int)((g2 >> (8 * j)) & 0xFF);
+            o->q[32 * ib + 8 * l + j] = (int16_t)((sg & (1u << j)) ? -v1 : v1);
+            o->q[32 * ib + 8 * l + j + 4] = (int16_t)((sg & (1u << (j + 4))) ? -v2 : v2);
+          }
+        }
+      }
+      return 0;
+    }
     case QREF_IQ4_XS: {
       o->d = qref_fp16_to_f32(rd16(p));
       const unsigned sh = rd16(p + 2);
@@ -204,7 +285,7 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
 
 int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
   const int r = decode_sb_raw(type, p, o);
-  if (r == 0 && type != QREF_Q6_K)
+  if (r == 0 && type != QREF_Q6_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
     for (int i = 0; i < 16; ++i) o->sc16[i] = o->sc[i / 2];
   return r;
 }
@@ -218,7 +299,8 @@ static float dequant_value(int type, const qref_sb* o, int e) {
     case QREF_Q4_0:
     case QREF_IQ4_NL: return o->d8[e / 32] * (float)o->q[e];
     case QREF_Q6_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
-    default: return o->d * (float)o->sc[e / 32] * (float)o->q[e] - 0.0f;
+    /* (the IQ types: o.wd * o.wsc[e / 16] * (o.q[e] - o.qoff) - 0 with qoff = 0, src/quants.h:322) */
+    default: return o->d * (float)o->sc16[e / 16] * (float)o->q[e] - 0.0f;
   }
 }
 

@@ -1,7 +1,7 @@
-"""Independent numpy encoders of the four GGUF block structs, written from the GGML block definitions
+"""Independent numpy encoders of the GGUF block structs, written from the GGML block definitions
 (ggml-common.h: block_q8_0 {d; qs[32]}, block_q4_K {d; dmin; scales[12]; qs[128]}, block_iq4_xs {d; scales_h;
 scales_l[4]; qs[128]}, block_iq3_s {d; qs[64]; qh[8]; signs[32]; scales[4]}, block_q6_k {ql[128]; qh[64];
-scales[16]; d}), NOT from the oracle's decoders: they
+scales[16]; d}, and the IQ2 / IQ3_XXS structs listed below), NOT from the oracle's decoders: they
 pack chosen integer fields into bytes, so decoding them back pins the decoders' bit positions."""
 import numpy as np
 
@@ -103,3 +103,53 @@ def enc_q4_0(d8, nib):
 
 
 enc_iq4_nl = enc_q4_0  # (the same block struct: f16 d + 32 nibbles; the nibbles index the IQ4_NL codebook)
+
+
+# ---- the IQ2 / IQ3_XXS codebook types (ggml-common.h: block_iq2_xxs {d; qs[32] as u16}, block_iq2_xs {d; qs[32] as
+# u16; scales[8]}, block_iq2_s {d; qs[64]; qh[8]; scales[8]}, block_iq3_xxs {d; qs[96]}). Sign groups of 8 elements
+# carry an even number of negatives in these formats: the stored 7 bits are the first 7 signs and the 8th is their
+# parity, so the encoders take 7-bit sign words.
+
+def _u32(v):
+    return np.array([v], dtype=np.uint32).view(np.uint8)
+
+
+def enc_iq2_xxs(d, scale_nib, gidx, sgn7):
+    """scale_nib: 8 four-bit scales (value 1 + 2 nib, per 32); gidx: 32 eight-bit grid indices (one per 8 elements,
+    in element order); sgn7: 32 seven-bit sign words -> 66 bytes"""
+    out = [_h(d)]
+    for ib in range(8):
+        a0 = sum(int(gidx[4 * ib + l]) << (8 * l) for l in range(4))
+        a1 = sum(int(sgn7[4 * ib + l]) << (7 * l) for l in range(4)) | (int(scale_nib[ib]) << 28)
+        out += [_u32(a0), _u32(a1)]
+    return np.concatenate(out)
+
+
+def enc_iq2_xs(d, scale_nib16, gidx, sgn7):
+    """scale_nib16: 16 four-bit scales (per 16 elements); gidx: 32 nine-bit grid indices; sgn7: 32 seven-bit sign
+    words -> 74 bytes"""
+    qs = np.array([(int(gidx[g]) & 511) | (int(sgn7[g]) << 9) for g in range(32)], dtype=np.uint16).view(np.uint8)
+    sc = np.array([(int(scale_nib16[2 * ib]) & 0xF) | ((int(scale_nib16[2 * ib + 1]) & 0xF) << 4) for ib in range(8)],
+                  dtype=np.uint8)
+    return np.concatenate([_h(d), qs, sc])
+
+
+def enc_iq2_s(d, scale_nib16, gidx, signs8):
+    """scale_nib16: 16 four-bit scales; gidx: 32 ten-bit grid indices; signs8: 32 sign bytes (bit j: element j of
+    the group negative; all 8 bits stored) -> 82 bytes"""
+    qs = np.array([int(g) & 0xFF for g in gidx], dtype=np.uint8)
+    qh = np.zeros(8, dtype=np.uint8)
+    for g in range(32):
+        ib, l = divmod(g, 4)
+        qh[ib] |= ((int(gidx[g]) >> 8) & 3) << (2 * l)
+    sc = np.array([(int(scale_nib16[2 * ib]) & 0xF) | ((int(scale_nib16[2 * ib + 1]) & 0xF) << 4) for ib in range(8)],
+                  dtype=np.uint8)
+    return np.concatenate([_h(d), qs, np.asarray(signs8, dtype=np.uint8), qh, sc])
+
+
+def enc_iq3_xxs(d, scale_nib, gidx, sgn7):
+    """scale_nib: 8 four-bit scales (per 32); gidx: 64 eight-bit grid indices (one per 4 elements); sgn7: 32 seven-bit
+    sign words (one per 8 elements) -> 98 bytes"""
+    qs = np.asarray(gidx, dtype=np.uint8)
+    ss = [_u32(sum(int(sgn7[4 * ib + l]) << (7 * l) for l in range(4)) | (int(scale_nib[ib]) << 28)) for ib in range(8)]
+    return np.concatenate([_h(d), qs] + ss)

@@ -43,7 +43,7 @@ def test_codebooks_match_published_and_invariants():
     txt = open(oracle.HERE + "/iq_tables.inc").read()
     kv = [int(v) for v in re.search(r"QM_IQ4NL_VALUES_INIT \{([^}]*)\}", txt).group(1).split(",")]
     assert kv == KV_PUBLISHED
-    grid = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt)]
+    grid = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", re.search(r"QM_IQ3S_GRID_INIT \{(.*?)\}", txt, re.S).group(1))]
     assert len(grid) == 512
     assert grid[0] == 0x01010101 and grid[1] == 0x01010103 and grid[-1] == 0x0F0F0101  # published end entries
     assert grid == sorted(grid) and len(set(grid)) == 512  # ggml's IQ3_S grid is sorted and distinct
@@ -109,7 +109,8 @@ def test_iq4_xs_decoder_round_trip_and_closed_form():
 def test_iq3_s_decoder_round_trip():
     import re
     txt = open(oracle.HERE + "/iq_tables.inc").read()
-    grid = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt)], dtype=np.int64)
+    body = re.search(r"QM_IQ3S_GRID_INIT \{(.*?)\}", txt, re.S).group(1)
+    grid = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", body)], dtype=np.int64)
     rng = np.random.default_rng(4)
     for it in range(50):
         d = np.float16(rng.random())
@@ -131,7 +132,8 @@ def test_iq3_s_decoder_round_trip():
         assert np.array_equal(w, ref)
 
 
-@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S, F.IQ2_XXS,
+                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS])
 def test_synth_weights_have_the_requested_statistics(qtype):
     W = F.synth_weight(qtype, 64, 512, seed=5)
     assert W.shape == (64, F.row_bytes(qtype, 512))
@@ -190,3 +192,89 @@ def test_q4_0_and_iq4_nl_decoders(qtype):
         assert np.array_equal(o["q"], q) and np.array_equal(o["d8"], d8)
         w = oracle.dequant_rows(qtype, raw[None], 256)[0]
         assert np.array_equal(w, (np.repeat(d8, 32) * q.astype(np.float32)).astype(np.float32))
+
+
+# ---- IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS
+def _grid(name, width):
+    import re
+    txt = open(oracle.HERE + "/iq_tables.inc").read()
+    body = re.search(name + r"_INIT \{(.*?)\}", txt, re.S).group(1)
+    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-f]+)u", body)]
+    return np.array(vals, dtype=np.uint64), width
+
+
+def _signs8(sgn7):
+    """the 8 sign bits of a 7-bit sign word: the 7 bits, then their parity (an even number of negatives)"""
+    s = np.asarray(sgn7, dtype=np.int64)
+    par = np.array([bin(int(v)).count("1") & 1 for v in s])
+    return s | (par << 7)
+
+
+def test_iq2_iq3xxs_codebooks_published_and_invariants():
+    g2xxs, _ = _grid("QM_IQ2XXS_GRID", 8)
+    g2xs, _ = _grid("QM_IQ2XS_GRID", 8)
+    g2s, _ = _grid("QM_IQ2S_GRID", 8)
+    g3xxs, _ = _grid("QM_IQ3XXS_GRID", 4)
+    assert (len(g2xxs), len(g2xs), len(g2s), len(g3xxs)) == (256, 512, 1024, 256)
+    # published first entries (ggml-common.h)
+    assert int(g2xxs[0]) == 0x0808080808080808 and int(g2xxs[1]) == 0x080808080808082b
+    assert int(g3xxs[0]) == 0x04040404 and int(g3xxs[1]) == 0x04040414
+    for g, w, allowed in ((g2xxs, 8, {8, 25, 43}), (g2xs, 8, {8, 25, 43}), (g2s, 8, {8, 25, 43}),
+                          (g3xxs, 4, {4, 12, 20, 28, 36, 44, 52, 62})):
+        assert len(set(g.tolist())) == len(g)  # distinct
+        vals = {(int(v) >> (8 * j)) & 0xFF for v in g for j in range(w)}
+        assert vals <= allowed
+    # the sign table is the 7 bits plus their parity (the table is data; this is the rule it follows)
+    import re
+    txt = open(oracle.HERE + "/iq_tables.inc").read()
+    ks = [int(v) for v in re.search(r"QM_KSIGNS_IQ2XS_INIT \{([^}]*)\}", txt).group(1).split(",")]
+    assert ks == _signs8(np.arange(128)).tolist()
+
+
+def _expect(grid, idx, width, signs8):
+    """elements of groups of `width` grid bytes with sign bytes signs8 (one per 8 elements)"""
+    mag = np.array([(int(grid[idx[e // width]]) >> (8 * (e % width))) & 0xFF for e in range(256)], dtype=np.int64)
+    neg = np.array([(int(signs8[e // 8]) >> (e % 8)) & 1 for e in range(256)], dtype=bool)
+    return np.where(neg, -mag, mag)
+
+
+@pytest.mark.parametrize("qtype", [F.IQ2_XXS, F.IQ2_XS, F.IQ2_S, F.IQ3_XXS])
+def test_iq2_iq3xxs_decoder_round_trip(qtype):
+    rng = np.random.default_rng(qtype * 11)
+    for it in range(30):
+        d = np.float16(rng.random() + 0.1)
+        if qtype == F.IQ2_XXS:
+            grid, _ = _grid("QM_IQ2XXS_GRID", 8)
+            nib = rng.integers(0, 16, 8)
+            gidx, sgn7 = rng.integers(0, 256, 32), rng.integers(0, 128, 32)
+            raw = enc.enc_iq2_xxs(d, nib, gidx, sgn7)
+            q, sc16, dd = _expect(grid, gidx, 8, _signs8(sgn7)), np.repeat(1 + 2 * nib, 2), np.float32(d) / 8
+        elif qtype == F.IQ2_XS:
+            grid, _ = _grid("QM_IQ2XS_GRID", 8)
+            nib16 = rng.integers(0, 16, 16)
+            gidx, sgn7 = rng.integers(0, 512, 32), rng.integers(0, 128, 32)
+            if it == 0:
+                gidx[:] = 256 + np.arange(32)  # the 9th index bit everywhere
+            raw = enc.enc_iq2_xs(d, nib16, gidx, sgn7)
+            q, sc16, dd = _expect(grid, gidx, 8, _signs8(sgn7)), 1 + 2 * nib16, np.float32(d) / 8
+        elif qtype == F.IQ2_S:
+            grid, _ = _grid("QM_IQ2S_GRID", 8)
+            nib16 = rng.integers(0, 16, 16)
+            gidx, signs8 = rng.integers(0, 1024, 32), rng.integers(0, 256, 32)
+            if it == 0:
+                gidx[:] = 768 + np.arange(32)  # both high index bits everywhere
+                signs8[:] = 255
+            raw = enc.enc_iq2_s(d, nib16, gidx, signs8)
+            q, sc16, dd = _expect(grid, gidx, 8, signs8), 1 + 2 * nib16, np.float32(d) / 8
+        else:
+            grid, _ = _grid("QM_IQ3XXS_GRID", 4)
+            nib = rng.integers(0, 16, 8)
+            gidx, sgn7 = rng.integers(0, 256, 64), rng.integers(0, 128, 32)
+            raw = enc.enc_iq3_xxs(d, nib, gidx, sgn7)
+            q, sc16, dd = _expect(grid, gidx, 4, _signs8(sgn7)), np.repeat(1 + 2 * nib, 2), np.float32(d) / 4
+        assert raw.size == F.SB_BYTES[qtype]
+        o = oracle.decode_sb(qtype, raw)
+        assert np.array_equal(o["q"], q) and np.array_equal(o["sc16"], sc16) and o["d"] == dd
+        w = oracle.dequant_rows(qtype, raw[None], 256)[0]
+        ref = (dd * sc16[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32)).astype(np.float32)
+        assert np.array_equal(w, ref)
