@@ -36,11 +36,28 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool known_type(int t) {
   return t == QM_Q4_0 || t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q5_K || t == QM_Q6_K || t == QM_IQ4_NL || t == QM_IQ3_S ||
-         t == QM_IQ4_XS;
+         t == QM_IQ4_XS || t == QM_IQ2_XXS || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_IQ3_XXS;
 }
 
-int payload_bytes(int t) { return t == QM_Q8_0 ? 32 : t == QM_IQ3_S ? 12 : t == QM_Q6_K ? 24 : t == QM_Q5_K ? 20 : 16; }
-int header_bytes(int t) { return t == QM_IQ4_XS ? 8 : t == QM_Q6_K ? 20 : 16; }
+int payload_bytes(int t) {
+  switch (t) {
+    case QM_Q8_0: return 32;
+    case QM_Q6_K: return 24;
+    case QM_Q5_K: return 20;
+    case QM_IQ3_S: case QM_IQ3_XXS: return 12;
+    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: return 8;
+    default: return 16;
+  }
+}
+int header_bytes(int t) {
+  switch (t) {
+    case QM_IQ4_XS: return 8;
+    case QM_Q6_K: case QM_IQ2_S: return 20;
+    case QM_IQ2_XS: return 12;
+    case QM_IQ2_XXS: case QM_IQ3_XXS: return 4;
+    default: return 16;
+  }
+}
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -135,6 +152,10 @@ size_t qmatmul_sb_bytes(int type) {
     case QM_IQ4_NL: return 144;
     case QM_IQ3_S: return 110;
     case QM_IQ4_XS: return 136;
+    case QM_IQ2_XXS: return 66;
+    case QM_IQ2_XS: return 74;
+    case QM_IQ2_S: return 82;
+    case QM_IQ3_XXS: return 98;
     default: return 0;
   }
 }
@@ -417,8 +438,10 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
   for (const qm_weight* w : {gate, up, down})
-    if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K)
-      return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: Q4_K, Q5_K and Q6_K expert weights (per-16 sums) are not supported");
+    if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K || w->type == QM_IQ2_XS || w->type == QM_IQ2_S)
+      return fail(QM_ERR_TYPE,
+                  "qmatmul_moe_grouped: Q4_K, Q5_K, Q6_K, IQ2_XS and IQ2_S expert weights (per-16 sums or scales) are "
+                  "not supported");
   if (gate->type != up->type)
     return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: gate and up must have one type (got %d, %d)", gate->type, up->type);
   if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)

@@ -7,6 +7,18 @@ namespace qm {
 
 template <int TYPE> struct LdsFor { struct type { int unused; }; };
 template <> struct LdsFor<T_IQ3_S> { using type = Iq3Lds; };
+template <> struct LdsFor<T_IQ2_XXS> { using type = IqLds<T_IQ2_XXS>; };
+template <> struct LdsFor<T_IQ2_XS> { using type = IqLds<T_IQ2_XS>; };
+template <> struct LdsFor<T_IQ2_S> { using type = IqLds<T_IQ2_S>; };
+template <> struct LdsFor<T_IQ3_XXS> { using type = IqLds<T_IQ3_XXS>; };
+
+// Fills a work-group's LDS tables for TYPE (nothing for the types without codebooks in LDS); the caller
+// synchronizes before use.
+template <int TYPE>
+__device__ __forceinline__ void lds_fill(typename LdsFor<TYPE>::type* t) {
+  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(t);
+  else if constexpr (kIq2<TYPE>) iq_lds_fill<TYPE>(t);
+}
 
 // The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0, Q5_K and Q6_K also q1) and header (h).
 // (native vector members: arrays of structs holding HIP's uint4 are kept in scratch memory)
@@ -41,6 +53,23 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
     r.q1.y = __builtin_nontemporal_load(q + 1);
     r.h.x = ((const uint16_t*)hp)[b & 7];  // the block's two int8 scales
     r.h.y = ((const uint16_t*)hp)[8];      // f16 d
+  } else if constexpr (kIq2<TYPE>) {
+    // (payload words q0.x..z; header: IQ2_XS scales in h.x, h.y and d in h.z, IQ2_S qh in h.x, h.y, scales in
+    //  h.z, h.w and d in q1.x, the others d in h.x)
+    const uint32_t* q = (const uint32_t*)qp;
+    r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
+                   TYPE == T_IQ3_XXS ? __builtin_nontemporal_load(q + 2) : 0u, 0u};
+    const uint32_t* hw = (const uint32_t*)hp;
+    if constexpr (TYPE == T_IQ2_XS) {
+      r.h.x = hw[0];
+      r.h.y = hw[1];
+      r.h.z = hw[2];
+    } else if constexpr (TYPE == T_IQ2_S) {
+      r.h = *(const u32x4_t*)hp;
+      r.q1.x = hw[4];
+    } else {
+      r.h.x = hw[0];
+    }
   } else if constexpr (TYPE == T_IQ3_S) {
     const uint32_t* q = (const uint32_t*)qp;
     r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2),
@@ -66,7 +95,7 @@ __device__ __forceinline__ RawBlk load_block(const WView& w, int n, int b) {
 }
 
 // Decodes a loaded 32-block (index ib = b % 8 in its superblock): w[k] = elements 4k..4k+3 (int8x4), the integer
-// scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K), the min mn, the float scales d (and dmin). Q6_K's
+// scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K, IQ2_XS and IQ2_S), the min mn, the float scales d (and dmin). Q6_K's
 // values come out as the stored 6-bit numbers 0..63 (the offset of 32 is removed by block_product).
 template <int TYPE>
 __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int ib,
@@ -152,6 +181,20 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     iq3s_pair<3>(lds, r.q0.x, r.q0.y, qh, r.q0.z, wd[6], wd[7]);
     sc = 1 + 2 * (int)((r.h.z >> (4 * ib)) & 0xFu);
     d = h2f(r.h.w);
+  } else if constexpr (kIq2<TYPE>) {
+    const uint32_t qh = TYPE == T_IQ2_S ? ((ib < 4 ? r.h.x : r.h.y) >> (8 * (ib & 3))) & 0xFFu : 0u;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) iq_group<TYPE>(lds, r.q0.x, r.q0.y, r.q0.z, qh, l, wd[2 * l], wd[2 * l + 1]);
+    if constexpr (Traits<TYPE>::SPLIT) {
+      const uint32_t sb = TYPE == T_IQ2_XS ? (((ib < 4 ? r.h.x : r.h.y) >> (8 * (ib & 3))) & 0xFFu)
+                                           : (((ib < 4 ? r.h.z : r.h.w) >> (8 * (ib & 3))) & 0xFFu);
+      sc = 1 + 2 * (int)(sb & 0xFu);
+      sc1 = 1 + 2 * (int)(sb >> 4);
+      d = h2f(TYPE == T_IQ2_XS ? r.h.z : r.q1.x) * kIqDScale<TYPE>;
+      return;
+    }
+    sc = 1 + 2 * (int)((TYPE == T_IQ2_XXS ? r.q0.y : r.q0.z) >> 28);
+    d = h2f(r.h.x) * kIqDScale<TYPE>;
   }
   sc1 = sc;
 }
@@ -181,6 +224,8 @@ __device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1,
   if constexpr (Traits<TYPE>::SC16) {
     // (|lo - 32 bs| < 2^17 and |sc| < 2^7: the 24-bit multiplies are exact)
     iv = __mul24(sc, lo - 32 * bs0) + __mul24(sc1, hi - 32 * bs1);
+  } else if constexpr (Traits<TYPE>::SPLIT) {
+    iv = __mul24(sc, lo) + __mul24(sc1, hi);
   } else if constexpr (kBlockScales<TYPE>) {
     iv = lo + hi;
   } else {

@@ -15,6 +15,10 @@
 //   Q4_0, IQ4_NL QB 16: byte t = n[t] | n[16+t] << 4 (GGUF order)       HB 16: the 8 blocks' f16 scales (as Q8_0)
 //   Q6_K   QB 24: byte t = low4[t] | low4[16+t] << 4, then two words of 2-bit high parts: word h (h = 0, 1),
 //                 byte i, bits 2k..2k+1 = high2[16h + 4k + i]          HB 20: int8 scales[16] (per 16), f16 d, 2 zero
+//   IQ2_XXS QB 8: GGUF a0 (4 grid indices), a1 (4 x 7-bit sign indices, 4-bit scale)   HB 4: f16 d, 2 zero
+//   IQ2_XS  QB 8: GGUF qs[4] (u16: 9-bit grid index | 7-bit sign index << 9)  HB 12: scales[8], f16 d, 2 zero
+//   IQ2_S   QB 8: 4 grid index low bytes, 4 sign bytes          HB 20: qh[8], scales[8], f16 d, 2 zero
+//   IQ3_XXS QB 12: 8 grid index bytes, GGUF sign/scale word (4 x 7-bit sign indices, 4-bit scale)  HB 4: f16 d, 2 zero
 // (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
 // (Q4_K's GGUF nibble order -- 64-element chunks, low nibbles first -- is regrouped to IQ4_XS's per-32 order, so
 // the 4-bit types share one unpacking path.)
@@ -27,23 +31,33 @@
 
 namespace qm {
 
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ4_XS = 23 };
+enum : int {
+  T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17, T_IQ3_XXS = 18,
+  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23
+};
 
 template <int TYPE> struct Traits;
 // MINS: per-block mins (the activation block sums enter the result); SC16: two integer scales per 32-block (one per
-// 16) and quants stored with an offset of 32 (removed with the per-16 activation sums)
-template <> struct Traits<T_Q8_0> { static constexpr int QB = 32, HB = 16, GGUF_SB = 272; static constexpr bool MINS = false, SC16 = false; };
-template <> struct Traits<T_Q4_K> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = true, SC16 = false; };
-template <> struct Traits<T_Q5_K> { static constexpr int QB = 20, HB = 16, GGUF_SB = 176; static constexpr bool MINS = true, SC16 = false; };
-template <> struct Traits<T_Q4_0> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false; };
-template <> struct Traits<T_IQ4_NL> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false; };
-template <> struct Traits<T_Q6_K> { static constexpr int QB = 24, HB = 20, GGUF_SB = 210; static constexpr bool MINS = false, SC16 = true; };
-template <> struct Traits<T_IQ4_XS> { static constexpr int QB = 16, HB = 8, GGUF_SB = 136; static constexpr bool MINS = false, SC16 = false; };
-template <> struct Traits<T_IQ3_S> { static constexpr int QB = 12, HB = 16, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false; };
+// 16) and quants stored with an offset of 32 (removed with the per-16 activation sums); SPLIT: two integer scales per
+// 32-block, signed quants (no offset)
+template <> struct Traits<T_Q8_0> { static constexpr int QB = 32, HB = 16, GGUF_SB = 272; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_Q4_K> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = true, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_Q5_K> { static constexpr int QB = 20, HB = 16, GGUF_SB = 176; static constexpr bool MINS = true, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_Q4_0> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_IQ4_NL> { static constexpr int QB = 16, HB = 16, GGUF_SB = 144; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_Q6_K> { static constexpr int QB = 24, HB = 20, GGUF_SB = 210; static constexpr bool MINS = false, SC16 = true, SPLIT = false; };
+template <> struct Traits<T_IQ4_XS> { static constexpr int QB = 16, HB = 8, GGUF_SB = 136; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_IQ3_S> { static constexpr int QB = 12, HB = 16, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_IQ2_XXS> { static constexpr int QB = 8, HB = 4, GGUF_SB = 66; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_IQ2_XS> { static constexpr int QB = 8, HB = 12, GGUF_SB = 74; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
+template <> struct Traits<T_IQ2_S> { static constexpr int QB = 8, HB = 20, GGUF_SB = 82; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
+template <> struct Traits<T_IQ3_XXS> { static constexpr int QB = 12, HB = 4, GGUF_SB = 98; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
 // per-32 f16 scales in the header (Q8_0's layout), no integer sub-scales
 template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL;
 // whether the kernels need the per-16 activation sums (absum)
 template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
+// the codebook types whose tables live in LDS
+template <int TYPE> constexpr bool kIq2 = TYPE == T_IQ2_XXS || TYPE == T_IQ2_XS || TYPE == T_IQ2_S || TYPE == T_IQ3_XXS;
 
 // A prepared weight as the kernels see it.
 struct WView {
@@ -180,6 +194,79 @@ __device__ __forceinline__ void iq3s_pair(const Iq3Lds* t, uint32_t q0, uint32_t
   w0 = (t->grid[i1] ^ m.x) + m.z;
   w1 = (t->grid[i2] ^ m.y) + m.w;
 }
+
+// ---- the 2-bit / IQ3_XXS codebook types (src/quants.h:170-239)
+// Device-resident codebooks (ggml's, see iq_tables.inc) and the 7-bit sign index -> sign byte table (the 8th sign is
+// the parity of the 7 stored ones).
+static __device__ const uint64_t g_iq2xxs_grid[256] = QM_IQ2XXS_GRID_INIT;
+static __device__ const uint64_t g_iq2xs_grid[512] = QM_IQ2XS_GRID_INIT;
+static __device__ const uint64_t g_iq2s_grid[1024] = QM_IQ2S_GRID_INIT;
+static __device__ const uint32_t g_iq3xxs_grid[256] = QM_IQ3XXS_GRID_INIT;
+
+template <int TYPE> struct IqGrid;
+template <> struct IqGrid<T_IQ2_XXS> { using G = uint2; static constexpr int NG = 256, NS = 128; };
+template <> struct IqGrid<T_IQ2_XS> { using G = uint2; static constexpr int NG = 512, NS = 128; };
+template <> struct IqGrid<T_IQ2_S> { using G = uint2; static constexpr int NG = 1024, NS = 256; };
+template <> struct IqGrid<T_IQ3_XXS> { using G = uint32_t; static constexpr int NG = 256, NS = 128; };
+
+// LDS copies of a type's grid and its sign masks (indexed by the stored sign field: 7 bits, IQ2_S 8 bits):
+// IQ2_XXS 4 KB, IQ2_XS 6 KB, IQ2_S 12 KB, IQ3_XXS 3 KB per work-group.
+template <int TYPE> struct IqLds {
+  typename IqGrid<TYPE>::G grid[IqGrid<TYPE>::NG];
+  uint4 sgn[IqGrid<TYPE>::NS];
+};
+template <int TYPE>
+__device__ __forceinline__ void iq_lds_fill(IqLds<TYPE>* t) {
+  using I = IqGrid<TYPE>;
+  for (int i = threadIdx.x; i < I::NG; i += blockDim.x) {
+    if constexpr (TYPE == T_IQ3_XXS) {
+      t->grid[i] = g_iq3xxs_grid[i];
+    } else {
+      const uint64_t g = TYPE == T_IQ2_XXS ? g_iq2xxs_grid[i] : TYPE == T_IQ2_XS ? g_iq2xs_grid[i] : g_iq2s_grid[i];
+      t->grid[i] = make_uint2((uint32_t)g, (uint32_t)(g >> 32));
+    }
+  }
+  for (int i = threadIdx.x; i < I::NS; i += blockDim.x) {
+    const uint32_t sb = I::NS == 128 ? (uint32_t)i | ((__builtin_popcount(i) & 1u) << 7) : (uint32_t)i;
+    const SgnMask m = sign_mask_of(sb);
+    t->sgn[i] = make_uint4(m.m0, m.m1, m.x0, m.x1);
+  }
+}
+
+// Group l (elements 8l..8l+7, l = 0..3) of a 32-block -> two signed int8x4 words, from the block's payload words
+// p0, p1, p2 (prepared layout above) and, for IQ2_S, its qh byte. Grid bytes are >= 4, so (g ^ m) + x negates the
+// masked bytes without carries.
+template <int TYPE>
+__device__ __forceinline__ void iq_group(const IqLds<TYPE>* t, uint32_t p0, uint32_t p1, uint32_t p2, uint32_t qh,
+                                         int l, uint32_t& w0, uint32_t& w1) {
+  if constexpr (TYPE == T_IQ3_XXS) {
+    const uint32_t qw = l < 2 ? p0 : p1;
+    const int sh = 16 * (l & 1);
+    const uint4 m = t->sgn[(p2 >> (7 * l)) & 127u];
+    w0 = (t->grid[(qw >> sh) & 0xFFu] ^ m.x) + m.z;
+    w1 = (t->grid[(qw >> (sh + 8)) & 0xFFu] ^ m.y) + m.w;
+  } else {
+    uint32_t gi, si;
+    if constexpr (TYPE == T_IQ2_XXS) {
+      gi = (p0 >> (8 * l)) & 0xFFu;
+      si = (p1 >> (7 * l)) & 127u;
+    } else if constexpr (TYPE == T_IQ2_XS) {
+      const uint32_t q16 = ((l < 2 ? p0 : p1) >> (16 * (l & 1))) & 0xFFFFu;
+      gi = q16 & 511u;
+      si = q16 >> 9;
+    } else {
+      gi = ((p0 >> (8 * l)) & 0xFFu) | ((qh << (8 - 2 * l)) & 0x300u);
+      si = (p1 >> (8 * l)) & 0xFFu;
+    }
+    const uint2 g = t->grid[gi];
+    const uint4 m = t->sgn[si];
+    w0 = (g.x ^ m.x) + m.z;
+    w1 = (g.y ^ m.y) + m.w;
+  }
+}
+
+// Per-type scale unit: IQ2 d / 8, IQ3_XXS d / 4 (src/quants.h:172, 222) -- exact powers of two
+template <int TYPE> constexpr float kIqDScale = TYPE == T_IQ3_XXS ? 0.25f : 0.125f;
 
 // ---- wave-level reductions (wave64)
 __device__ __forceinline__ float wave_sum_width(float v, int width) {

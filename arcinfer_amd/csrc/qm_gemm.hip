@@ -15,7 +15,7 @@
 // The 32x32 MFMA result layout: lane l holds column j = l % 32 and rows 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
 #include <stdlib.h>
 
-#include "qm_launch.h"
+#include "qm_decode.h"
 
 namespace qm {
 
@@ -32,7 +32,7 @@ template <int TYPE, int MT> struct GemmLds {
   alignas(16) float asc[2][8 * 32 * MT];
   float u[2][Traits<TYPE>::MINS ? 8 * 32 * MT : 1];
   int arow[32 * MT];
-  typename std::conditional<TYPE == T_IQ3_S, Iq3Lds, int>::type iq3;
+  typename LdsFor<TYPE>::type tab;  // (IQ3_S and the IQ2 / IQ3_XXS types: codebook and sign tables)
 };
 
 // IQ3_S, pair L (elements 8L..8L+7) with L known only at run time.
@@ -59,9 +59,12 @@ __device__ __forceinline__ uint4 load_payload(const WView& w, int n, int blk, in
   } else if constexpr (TYPE == T_Q5_K) {
     const uint2 nib = *(const uint2*)(qp + 8 * hf);
     return make_uint4(nib.x, nib.y, *(const uint32_t*)(qp + 16), 0u);
-  } else if constexpr (TYPE == T_IQ3_S) {
+  } else if constexpr (TYPE == T_IQ3_S || TYPE == T_IQ3_XXS) {
     const uint32_t* q = (const uint32_t*)qp;
     return make_uint4(q[0], q[1], q[2], 0u);
+  } else if constexpr (Traits<TYPE>::QB == 8) {
+    const uint2 q = *(const uint2*)qp;
+    return make_uint4(q.x, q.y, 0u, 0u);
   } else {
     return *(const uint4*)qp;
   }
@@ -73,6 +76,8 @@ __device__ __forceinline__ uint4 load_header(const WView& w, int n, int s) {
   if constexpr (TYPE == T_IQ4_XS) {
     const uint2 h = *(const uint2*)hp;
     return make_uint4(h.x, h.y, 0u, 0u);
+  } else if constexpr (Traits<TYPE>::HB == 4) {
+    return make_uint4(*(const uint32_t*)hp, 0u, 0u, 0u);
   } else {
     return *(const uint4*)hp;
   }
@@ -80,7 +85,8 @@ __device__ __forceinline__ uint4 load_header(const WView& w, int n, int s) {
 
 // The MFMA B operand (16 int8 weights of k-half hf) from a lane's payload of 32-block b of its superblock.
 template <int TYPE>
-__device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, const KvTab& kv, const Iq3Lds* iq3) {
+__device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, const KvTab& kv,
+                                         const typename LdsFor<TYPE>::type* tab) {
   v4i r;
   if constexpr (TYPE == T_Q8_0) {
     r[0] = (int)q.x; r[1] = (int)q.y; r[2] = (int)q.z; r[3] = (int)q.w;
@@ -91,6 +97,11 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
     const uint32_t hb = q.z >> (4 * hf);
 #pragma unroll
     for (int k = 0; k < 4; ++k) r[k] |= (int)(((hb >> k) & 0x01010101u) << 4);
+  } else if constexpr (kIq2<TYPE>) {
+    uint32_t w0, w1, w2, w3;
+    iq_group<TYPE>(tab, q.x, q.y, q.z, 0u, 2 * hf, w0, w1);
+    iq_group<TYPE>(tab, q.x, q.y, q.z, 0u, 2 * hf + 1, w2, w3);
+    r[0] = (int)w0; r[1] = (int)w1; r[2] = (int)w2; r[3] = (int)w3;
   } else if constexpr (TYPE != T_IQ3_S) {
     const int sh = 4 * hf;
     const uint32_t x0 = q.x >> sh, x1 = q.y >> sh, x2 = q.z >> sh, x3 = q.w >> sh;
@@ -107,18 +118,27 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
   } else {
     const uint32_t qh = ((b < 4 ? hdr.x : hdr.y) >> (8 * (b & 3))) & 0xFFu;
     uint32_t w0, w1, w2, w3;
-    iq3s_pair_rt(iq3, q.x, q.y, qh, q.z, 2 * hf, w0, w1);
-    iq3s_pair_rt(iq3, q.x, q.y, qh, q.z, 2 * hf + 1, w2, w3);
+    iq3s_pair_rt(tab, q.x, q.y, qh, q.z, 2 * hf, w0, w1);
+    iq3s_pair_rt(tab, q.x, q.y, qh, q.z, 2 * hf + 1, w2, w3);
     r[0] = (int)w0; r[1] = (int)w1; r[2] = (int)w2; r[3] = (int)w3;
   }
   return r;
 }
 
-// Per-block weight scales of one superblock from its header: dsc[b] = d * sc_b (Q8_0: the block's f16 scale),
-// dmn[b] = dmin * mn_b (Q4_K), isc[b] = the integer scale.
+// Per-block weight scales of one superblock from its header (IQ2_XXS, IQ3_XXS: and its blocks' payloads pay, whose
+// last word holds the 4-bit scale): dsc[b] = d * sc_b (Q8_0: the block's f16 scale), dmn[b] = dmin * mn_b (Q4_K),
+// isc[b] = the integer scale.
 template <int TYPE>
-__device__ __forceinline__ void sb_scales(uint4 h, float dsc[8], float dmn[8], int isc[8]) {
-  if constexpr (kBlockScales<TYPE>) {
+__device__ __forceinline__ void sb_scales(uint4 h, const uint4* pay, float dsc[8], float dmn[8], int isc[8]) {
+  if constexpr (TYPE == T_IQ2_XXS || TYPE == T_IQ3_XXS) {
+    const float d = h2f(h.x) * kIqDScale<TYPE>;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      isc[b] = 1 + 2 * (int)((TYPE == T_IQ2_XXS ? pay[b].y : pay[b].z) >> 28);
+      dsc[b] = d * (float)isc[b];
+      dmn[b] = 0.0f;
+    }
+  } else if constexpr (kBlockScales<TYPE>) {
     const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -213,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     else src = m0 + i;
     L.arow[tid] = src;
   }
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&L.iq3);
+  lds_fill<TYPE>(&L.tab);
   const KvTab kv = kv_tab();
   const uint32_t hfm = 0u - (uint32_t)hf;  // all ones in the upper half-wave
   __syncthreads();
@@ -294,8 +314,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
     float dsc[8], dmn[8], dsc2[8], dmn2[8];
     int isc[8], isc2[8];
-    sb_scales<TYPE>(hdr, dsc, dmn, isc);
-    if constexpr (GU) sb_scales<TYPE>(hdr2, dsc2, dmn2, isc2);
+    sb_scales<TYPE>(hdr, pay, dsc, dmn, isc);
+    if constexpr (GU) sb_scales<TYPE>(hdr2, pay2, dsc2, dmn2, isc2);
     const uint4 hcur = hdr, hcur2 = hdr2;
     hdr = load_header<TYPE>(a.w, n, sn);
     if constexpr (GU) hdr2 = load_header<TYPE>(a.w2, n, sn);
@@ -315,10 +335,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int b = 2 * p + q;
-        bop[q] = b_operand<TYPE>(pay[b], hcur, b, hf, kv, (const Iq3Lds*)&L.iq3);
+        bop[q] = b_operand<TYPE>(pay[b], hcur, b, hf, kv, &L.tab);
         pay[b] = load_payload<TYPE>(a.w, n, sn * 8 + b, hf);
         if constexpr (GU) {
-          bop2[q] = b_operand<TYPE>(pay2[b], hcur2, b, hf, kv, (const Iq3Lds*)&L.iq3);
+          bop2[q] = b_operand<TYPE>(pay2[b], hcur2, b, hf, kv, &L.tab);
           pay2[b] = load_payload<TYPE>(a.w2, n, sn * 8 + b, hf);
         }
       }
@@ -461,19 +481,19 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Q6_K prompt GEMM. Q6_K has an integer scale per 16 elements, so each 32-block needs its two halves' int32 sums
-// separately (the reference's sc0 * lo + sc1 * hi): two v_mfma_i32_32x32x16_i8 per block and row tile, lane half h
-// holding elements 8h..8h+7 of each 16-element half. The B operand is decoded in registers to signed int8 (the 6-bit
-// value minus 32, a byte-wise subtract without borrows); one 2-block f32 outer product gives asc * d * sc for both
-// halves (lanes 0-31: the first half's scale, lanes 32-63: the second's). Tiles, staging and epilogue as
-// gemm_kernel's dense mode.
-template <int MT, bool DUMP>
-__global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
+// Prompt GEMM of the types with an integer scale per 16 elements (Q6_K, IQ2_XS, IQ2_S): each 32-block needs its two
+// halves' int32 sums separately (the reference's sc0 * lo + sc1 * hi): two v_mfma_i32_32x32x16_i8 per block and row
+// tile, lane half h holding elements 8h..8h+7 of each 16-element half. The B operand is decoded in registers to
+// signed int8 (Q6_K: the 6-bit value minus 32, a byte-wise subtract without borrows; IQ2: grid words with their
+// signs, groups h and 2 + h of the block); one 2-block f32 outer product gives asc * d * sc for both halves (lanes
+// 0-31: the first half's scale, lanes 32-63: the second's). Tiles, staging and epilogue as gemm_kernel's dense mode.
+template <int TYPE, int MT, bool DUMP>
+__global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
   constexpr int BM = 32 * MT;
   constexpr int ACH = BM * 16 / 256;
   constexpr int SCH = (8 * BM + 255) / 256;
-  using Tr = Traits<T_Q6_K>;
-  __shared__ GemmLds<T_Q6_K, MT> L;
+  using Tr = Traits<TYPE>;
+  __shared__ GemmLds<TYPE, MT> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
   const int K = a.w.K, nb = K / 32, nsb = K / 256;
   int nt, mtile;
@@ -482,6 +502,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
   const int n_loc = nt * 128 + wave * 32 + lc, n_rows = a.w.rows;
   const int n = min(n_loc, n_rows - 1);
   if (tid < BM) L.arow[tid] = m0 + min(tid, nvalid - 1);
+  lds_fill<TYPE>(&L.tab);
   __syncthreads();
 
   u32x4_t st_a[ACH];
@@ -514,22 +535,34 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
       }
     }
   };
-  // this lane's share of a block: nibble bytes 8h..8h+7 and both 2-bit words (record: 16 nibble bytes, 2 words)
+  // this lane's share of a block: Q6_K nibble bytes 8h..8h+7 and both 2-bit words (record: 16 nibble bytes, 2
+  // words); IQ2_XS / IQ2_S the block's whole 8-byte record (nib)
   const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
   const uint8_t* hrow = a.w.hdr + (size_t)n * nsb * Tr::HB;
   auto load_blk = [&](int blk, uint2& nib, uint2& hw) {
     const uint8_t* r = qrow + (size_t)blk * Tr::QB;
-    nib = *(const uint2*)(r + 8 * hf);
-    hw = *(const uint2*)(r + 16);
+    if constexpr (TYPE == T_Q6_K) {
+      nib = *(const uint2*)(r + 8 * hf);
+      hw = *(const uint2*)(r + 16);
+    } else {
+      nib = *(const uint2*)r;
+      hw = make_uint2(0u, 0u);
+    }
   };
   uint2 nib[8], hw[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) load_blk(b, nib[b], hw[b]);
-  // (header records are 20 bytes: 4-byte aligned, so read as dwords)
+  // (header records are 20 or 12 bytes: 4-byte aligned, so read as dwords) sc: Q6_K int8 scales[16], IQ2_XS
+  // scales[8] (.x .y), IQ2_S qh[8] (.x .y) and scales[8] (.z .w); dd: f16 d
   auto load_hdr = [&](int sb, uint4& sc, uint32_t& dd) {
     const uint32_t* h = (const uint32_t*)(hrow + (size_t)sb * Tr::HB);
-    sc = make_uint4(h[0], h[1], h[2], h[3]);  // int8 scales[16]
-    dd = h[4];                                // f16 d
+    if constexpr (TYPE == T_IQ2_XS) {
+      sc = make_uint4(h[0], h[1], 0u, 0u);
+      dd = h[2];
+    } else {
+      sc = make_uint4(h[0], h[1], h[2], h[3]);
+      dd = h[4];
+    }
   };
   uint4 hsc;
   uint32_t hd;
@@ -552,24 +585,34 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
     const int sn = s + 1 < nsb ? s + 1 : s;
     fetch(sn);
     const uint32_t scw[4] = {hsc.x, hsc.y, hsc.z, hsc.w};
-    const float d = h2f(hd);
+    const float d = TYPE == T_Q6_K ? h2f(hd) : h2f(hd) * kIqDScale<TYPE>;
     load_hdr(sn, hsc, hd);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       if (b == 4) store(cur ^ 1);
       // B operands: elements 8hf..8hf+7 of the block's first half (o0) and of its second half (o1), signed
-      const uint32_t A2 = hf ? hw[b].x : hw[b].x << 4, B2 = hf ? hw[b].y : hw[b].y << 4;
       uint32_t w[4];
-      w[0] = (nib[b].x & 0x0F0F0F0Fu) | (A2 & 0x30303030u);
-      w[1] = (nib[b].y & 0x0F0F0F0Fu) | ((A2 >> 2) & 0x30303030u);
-      w[2] = ((nib[b].x >> 4) & 0x0F0F0F0Fu) | (B2 & 0x30303030u);
-      w[3] = ((nib[b].y >> 4) & 0x0F0F0F0Fu) | ((B2 >> 2) & 0x30303030u);
+      int sc0, sc1;
+      if constexpr (TYPE == T_Q6_K) {
+        const uint32_t A2 = hf ? hw[b].x : hw[b].x << 4, B2 = hf ? hw[b].y : hw[b].y << 4;
+        w[0] = (nib[b].x & 0x0F0F0F0Fu) | (A2 & 0x30303030u);
+        w[1] = (nib[b].y & 0x0F0F0F0Fu) | ((A2 >> 2) & 0x30303030u);
+        w[2] = ((nib[b].x >> 4) & 0x0F0F0F0Fu) | (B2 & 0x30303030u);
+        w[3] = ((nib[b].y >> 4) & 0x0F0F0F0Fu) | ((B2 >> 2) & 0x30303030u);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) w[k] = ((w[k] | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        for (int k = 0; k < 4; ++k) w[k] = ((w[k] | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
+        sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
+      } else {
+        const uint32_t qh = TYPE == T_IQ2_S ? (scw[b >> 2] >> (8 * (b & 3))) & 0xFFu : 0u;
+        iq_group<TYPE>(&L.tab, nib[b].x, nib[b].y, 0u, qh, hf, w[0], w[1]);
+        iq_group<TYPE>(&L.tab, nib[b].x, nib[b].y, 0u, qh, 2 + hf, w[2], w[3]);
+        const uint32_t sb = (scw[(TYPE == T_IQ2_S ? 2 : 0) + (b >> 2)] >> (8 * (b & 3))) & 0xFFu;
+        sc0 = 1 + 2 * (int)(sb & 0xFu);
+        sc1 = 1 + 2 * (int)(sb >> 4);
+      }
       const long o0 = (long)(((uint64_t)w[1] << 32) | w[0]), o1 = (long)(((uint64_t)w[3] << 32) | w[2]);
       load_blk(sn * 8 + b, nib[b], hw[b]);
-      const int sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
-      const int sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
       const float my_dsc = d * (float)(hf ? sc1 : sc0);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -621,10 +664,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(GemmArgs a) {
     }
 }
 
-template <int MT, bool DUMP>
-static hipError_t go_q6k(const GemmArgs& a, hipStream_t s) {
+template <int TYPE, int MT, bool DUMP>
+static hipError_t go_s16(const GemmArgs& a, hipStream_t s) {
   const unsigned gx = (unsigned)((a.w.rows + 127) / 128), gy = (unsigned)((a.M + 32 * MT - 1) / (32 * MT));
-  gemm_q6k_kernel<MT, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
+  gemm_s16_kernel<TYPE, MT, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -654,11 +697,19 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
   }
 }
 
+template <int TYPE>
+static hipError_t dispatch_s16(int mode, const GemmArgs& a, hipStream_t s) {
+  if (mode != GEMM_DENSE) return hipErrorInvalidValue;
+  if (a.dbg_isum) return go_s16<TYPE, 1, true>(a, s);
+  return a.M <= 32 ? go_s16<TYPE, 1, false>(a, s) : go_s16<TYPE, 2, false>(a, s);
+}
+
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
-  if (type == T_Q6_K) {
-    if (mode != GEMM_DENSE) return hipErrorInvalidValue;
-    if (a.dbg_isum) return go_q6k<1, true>(a, s);
-    return a.M <= 32 ? go_q6k<1, false>(a, s) : go_q6k<2, false>(a, s);
+  switch (type) {
+    case T_Q6_K: return dispatch_s16<T_Q6_K>(mode, a, s);
+    case T_IQ2_XS: return dispatch_s16<T_IQ2_XS>(mode, a, s);
+    case T_IQ2_S: return dispatch_s16<T_IQ2_S>(mode, a, s);
+    default: break;
   }
   switch (type) {
     case T_Q8_0: return dispatch<T_Q8_0>(mode, a, s);
@@ -668,6 +719,8 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
     case T_Q4_0: return dispatch<T_Q4_0>(mode, a, s);
     case T_IQ4_NL: return dispatch<T_IQ4_NL>(mode, a, s);
     case T_Q5_K: return mode == GEMM_DENSE ? dispatch<T_Q5_K>(mode, a, s) : hipErrorInvalidValue;
+    case T_IQ2_XXS: return dispatch<T_IQ2_XXS>(mode, a, s);
+    case T_IQ3_XXS: return dispatch<T_IQ3_XXS>(mode, a, s);
     default: return hipErrorInvalidValue;
   }
 }

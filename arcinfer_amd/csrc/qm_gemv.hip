@@ -15,6 +15,10 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_Q5_K: return gemv_dispatch<T_Q5_K>(a, s);
     case T_Q4_0: return gemv_dispatch<T_Q4_0>(a, s);
     case T_IQ4_NL: return gemv_dispatch<T_IQ4_NL>(a, s);
+    case T_IQ2_XXS: return gemv_dispatch<T_IQ2_XXS>(a, s);
+    case T_IQ2_XS: return gemv_dispatch<T_IQ2_XS>(a, s);
+    case T_IQ2_S: return gemv_dispatch<T_IQ2_S>(a, s);
+    case T_IQ3_XXS: return gemv_dispatch<T_IQ3_XXS>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -19,8 +19,8 @@ namespace qm {
 template <int TYPE, int LPR, int R, int TB, int U, bool DUMP>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ typename LdsFor<TYPE>::type lds;
-  if constexpr (TYPE == T_IQ3_S) {
-    iq3_lds_fill(&lds);
+  if constexpr (TYPE == T_IQ3_S || kIq2<TYPE>) {
+    lds_fill<TYPE>(&lds);
     __syncthreads();
   }
   constexpr int G = 64 / LPR;
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
   fetch(0, cur);
   // (the first weight loads are in flight while the activations are staged)
   __shared__ typename LdsFor<TYPE>::type lds;
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  lds_fill<TYPE>(&lds);
   for (int i = threadIdx.x; i < 2 * nb; i += 256) {
     const int b = i >> 1, h = i & 1;
     *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
     }
   };
   fetch(0, cur);
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  lds_fill<TYPE>(&lds);
   for (int i = threadIdx.x; i < 2 * nb * TB; i += 256) {
     const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
     const int tt = min(t, T - 1);  // (tokens past T: a copy of the last, never stored)
@@ -344,7 +344,7 @@ static hipError_t go1(const GemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
+template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S || kIq2<TYPE> ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
 static hipError_t go(const GemvArgs& a, hipStream_t s) {
   constexpr int rows_per_wg = 4 * (64 / LPR) * R;
   const dim3 grid((unsigned)((a.w.rows + rows_per_wg - 1) / rows_per_wg)), block(256);
@@ -369,8 +369,9 @@ hipError_t gemv_dispatch(const GemvArgs& a, hipStream_t s) {
     // tokens per launch: as many as fit in 80 KB of LDS (two work-groups per CU), up to 8; more tokens -> chunks
     // of tokens, each launch reading the weights once
     int tb = 8;
-    while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > 80 * 1024) tb >>= 1;
-    if (gemvs_lds(TYPE, a.w.K, tb) <= 80 * 1024) {
+    const size_t cap = 80 * 1024 - sizeof(typename LdsFor<TYPE>::type);  // (the codebook tables' static LDS)
+    while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > cap) tb >>= 1;
+    if (gemvs_lds(TYPE, a.w.K, tb) <= cap) {
       for (int t0 = 0; t0 < a.T; t0 += tb) {
         GemvArgs c = a;
         c.T = min(tb, a.T - t0);

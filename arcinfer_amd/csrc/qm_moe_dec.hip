@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
     rg[u] = load_block_at<TYPE>(gate.qs + row * nb * Tr::QB, gate.hdr + row * (nb / 8) * Tr::HB, b);
     ru[u] = load_block_at<TYPE>(up.qs + row * nb * Tr::QB, up.hdr + row * (nb / 8) * Tr::HB, b);
   }
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  lds_fill<TYPE>(&lds);
   for (int i = threadIdx.x; i < 2 * nb; i += 256) {
     const int b = i >> 1, hh = i & 1;
     *(uint4*)(sq + (size_t)hh * nb * 16 + b * 16) = *(const uint4*)(aq + (size_t)t * E + 32 * b + 16 * hh);
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
         r[k][u] = load_block_at<TYPE>(down.qs + row * nb * Tr::QB, down.hdr + row * (nb / 8) * Tr::HB,
                                       min(gl + LPR * u, nb - 1));
     }
-  if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(&lds);
+  lds_fill<TYPE>(&lds);
   // h rows of the token's NU slots, quantized per 32 (8 lanes per block: the quantizer's arithmetic)
   for (int b0 = 0; b0 < NU * nb; b0 += 32) {
     const int bi = b0 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
@@ -188,6 +188,8 @@ hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const
     case T_IQ3_S: return moe_dec_typed<T_IQ3_S>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     case T_Q4_0: return moe_dec_typed<T_Q4_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     case T_IQ4_NL: return moe_dec_typed<T_IQ4_NL>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ2_XXS: return moe_dec_typed<T_IQ2_XXS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ3_XXS: return moe_dec_typed<T_IQ3_XXS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     default: return hipErrorInvalidValue;
   }
 }

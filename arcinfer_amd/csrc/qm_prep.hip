@@ -95,6 +95,43 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     h[17] = p[209];
     h[18] = 0;
     h[19] = 0;
+  } else if constexpr (TYPE == T_IQ2_XXS || TYPE == T_IQ2_XS) {
+    // d | 8 blocks of 8 bytes (IQ2_XXS: a0, a1; IQ2_XS: four u16) [| IQ2_XS scales[8]]
+    for (int e = 0; e < 64; ++e) q[e] = p[2 + e];
+    if constexpr (TYPE == T_IQ2_XS) {
+      for (int e = 0; e < 8; ++e) h[e] = p[66 + e];
+      h[8] = p[0];
+      h[9] = p[1];
+      h[10] = 0;
+      h[11] = 0;
+    } else {
+      h[0] = p[0];
+      h[1] = p[1];
+      h[2] = 0;
+      h[3] = 0;
+    }
+  } else if constexpr (TYPE == T_IQ2_S) {
+    // d | qs[32] | signs[32] | qh[8] | scales[8]
+    for (int b = 0; b < 8; ++b)
+      for (int e = 0; e < 4; ++e) {
+        q[8 * b + e] = p[2 + 4 * b + e];
+        q[8 * b + 4 + e] = p[34 + 4 * b + e];
+      }
+    for (int e = 0; e < 16; ++e) h[e] = p[66 + e];
+    h[16] = p[0];
+    h[17] = p[1];
+    h[18] = 0;
+    h[19] = 0;
+  } else if constexpr (TYPE == T_IQ3_XXS) {
+    // d | qs[64] | 8 sign/scale words
+    for (int b = 0; b < 8; ++b) {
+      for (int e = 0; e < 8; ++e) q[12 * b + e] = p[2 + 8 * b + e];
+      for (int e = 0; e < 4; ++e) q[12 * b + 8 + e] = p[66 + 4 * b + e];
+    }
+    h[0] = p[0];
+    h[1] = p[1];
+    h[2] = 0;
+    h[3] = 0;
   } else {  // IQ3_S: d | qs[64] | qh[8] | signs[32] | scales[4]
     for (int b = 0; b < 8; ++b) {
       for (int e = 0; e < 8; ++e) q[12 * b + e] = p[2 + 8 * b + e];
@@ -121,6 +158,10 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t*
     case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     case T_IQ4_NL: repack_kernel<T_IQ4_NL><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ2_XXS: repack_kernel<T_IQ2_XXS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ2_XS: repack_kernel<T_IQ2_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ2_S: repack_kernel<T_IQ2_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_IQ3_XXS: repack_kernel<T_IQ3_XXS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -30,7 +30,8 @@ extern "C" {
 
 /* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
 typedef enum {
-  QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ4_XS = 23
+  QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ2_XXS = 16, QM_IQ2_XS = 17,
+  QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23
 } qm_type;
 
 typedef enum {
@@ -56,8 +57,8 @@ const char* qmatmul_last_error(void);
 /* Bytes of one 256-element superblock in GGUF (0 for an unsupported type); src/gguf.h:43-72. */
 size_t qmatmul_sb_bytes(int type);
 
-/* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S or Q6_K
- * superblock). */
+/* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S, Q6_K,
+ * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock). */
 size_t qmatmul_weight_bytes(int type, int rows, int K);
 
 /* Prepares a weight from its GGUF bytes: rows x (K/256) superblocks, row-major, as stored in a GGUF tensor (a
@@ -131,7 +132,8 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
  * gate, up: NE*F rows of E; down: NE*E rows of F (stacked experts). a_t: token t of aq/asc (E values). q(): the h
  * rows quantized per 32 as moe_quant (moe.cl:251-282). Route, exclusive scan into tiles, device-side scatter of
  * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
- * order (moe.cl:332-340). Gate/up/down types without per-block mins (Q8_0, IQ4_XS, IQ3_S). accumulate 0 or 1.
+ * order (moe.cl:332-340). Gate/up/down types with one integer scale per 32 and no mins (Q8_0, Q4_0, IQ4_NL, IQ4_XS,
+ * IQ3_S, IQ2_XXS, IQ3_XXS). accumulate 0 or 1.
  * ws: device workspace of at least qmatmul_moe_workspace_size bytes (layout: qmatmul_moe_ws_layout). */
 int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
                         int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,

@@ -69,7 +69,8 @@ def test_quantize_layout_padding_and_absum():
 
 
 # ---- int8 block-dot products
-@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S, F.IQ2_XXS,
+                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS])
 def test_blockdot_int_sums_brute_force(qtype):
     rng = np.random.default_rng(10 + qtype)
     N, K, M = 12, 512, 3
@@ -92,7 +93,8 @@ def test_blockdot_int_sums_brute_force(qtype):
                 assert np.array_equal(msum[m, n], mn * bs)
 
 
-@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S])
+@pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S, F.IQ2_XXS,
+                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS])
 def test_blockdot_f32_vs_dequantized_double(qtype):
     rng = np.random.default_rng(20 + qtype)
     N, K, M = 40, 1024, 4
