@@ -2,13 +2,15 @@
 
 Every expected value here is computed from the chosen integer FIELDS of each block (scales, nibbles, grid indices,
 sign bits) with numpy, following the GGML block definitions and the reference's per-element formulas
-(src/quants.h:149-158 Q8_0, 91-114 Q4_K / Q5_K, 115-135 Q6_K, 136-148 Q4_0 / IQ4_NL, 297-312 IQ4_XS, 240-262 IQ3_S;
+(src/quants.h:149-158 Q8_0, 91-114 Q4_K / Q5_K, 115-135 Q6_K, 136-148 Q4_0 / IQ4_NL, 297-312 IQ4_XS, 240-262 IQ3_S,
+170-239 IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS;
 quantizer 559-576; GEMV per-block expression zero/kernels/decode.cl:695-706). Nothing here calls the oracle or the product, so the fixture pins both.
 The block bytes come from tests/encoders.py (packing written from the GGML structs).
 
 Edge cases: d = 0, d = +-65504 (largest half), d = 2^-24 (smallest subnormal half), all-15 nibbles, IQ3_S grid
 indices with bit 8 set, all sign bits set, Q5_K with only the fifth bits set, all-0 and all-15 Q4_0 / IQ4_NL
-nibbles; quantizer rows with exact ties, zero blocks, +-amax, subnormals.
+nibbles, the IQ2 / IQ3_XXS types' last grid index with every stored sign set; quantizer rows with exact ties, zero
+blocks, +-amax, subnormals.
 
 Run: python tests/golden/make_golden.py   (deterministic; rewrites the .npz)
 """
@@ -27,13 +29,73 @@ F32 = np.float32
 D_EDGE = [0.0, 65504.0, -65504.0, 2.0 ** -24]
 
 
-def iq3s_grid():
+def _table(name):
+    """the integers of one #define'd initializer of oracle/iq_tables.inc (the codebooks are data, not arithmetic)"""
     txt = open(os.path.join(os.path.dirname(os.path.dirname(HERE)), "oracle", "iq_tables.inc")).read()
-    return np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt)], dtype=np.int64)
+    body = re.search(r"#define " + name + r" \{(.*?)\}", txt, re.S).group(1)
+    return np.array([int(v, 0) for v in re.findall(r"0x[0-9a-f]+|\d+", body)], dtype=np.uint64)
+
+
+def iq3s_grid():
+    return _table("QM_IQ3S_GRID_INIT").astype(np.int64)
+
+
+def _bytes_of(v, n):
+    return np.array([(int(v) >> (8 * j)) & 0xFF for j in range(n)], dtype=np.int64)
+
+
+def _sign8(s7):
+    """the 8 signs of a 7-bit sign word: bits 0-6 stored, bit 7 their parity (an even count of negatives)"""
+    bits = [(int(s7) >> j) & 1 for j in range(7)]
+    return np.array(bits + [sum(bits) & 1], dtype=bool)
+
+
+def iq2_superblocks(qtype, rng):
+    """IQ2_XXS (16), IQ2_XS (17), IQ2_S (22), IQ3_XXS (18) superblocks from chosen fields (src/quants.h:170-239):
+    value = (d / 8 or d / 4) * (1 + 2 * nibble) * (+-grid byte)"""
+    grid = {16: _table("QM_IQ2XXS_GRID_INIT"), 17: _table("QM_IQ2XS_GRID_INIT"), 22: _table("QM_IQ2S_GRID_INIT"),
+            18: _table("QM_IQ3XXS_GRID_INIT")}[qtype]
+    out = []
+    for i in range(len(D_EDGE) + 28):
+        d = np.float16(D_EDGE[i]) if i < len(D_EDGE) else np.float16(abs(rng.standard_normal()) * 0.01)
+        per16 = qtype in (17, 22)
+        nib = rng.integers(0, 16, 16 if per16 else 8)
+        if qtype == 18:
+            gidx = rng.integers(0, 256, 64)
+        else:
+            gidx = rng.integers(0, len(grid), 32)
+        sg = rng.integers(0, 256 if qtype == 22 else 128, 32)
+        if i == 1:  # largest index, all stored signs set, largest scale
+            gidx[:] = len(grid) - 1
+            sg[:] = 255 if qtype == 22 else 127
+            nib[:] = 15
+        if qtype == 18:
+            mag = np.concatenate([_bytes_of(grid[g], 4) for g in gidx])
+        else:
+            mag = np.concatenate([_bytes_of(grid[g], 8) for g in gidx])
+        neg = np.concatenate([np.array([(int(v) >> j) & 1 for j in range(8)], dtype=bool) if qtype == 22 else _sign8(v)
+                              for v in sg])
+        q = np.where(neg, -mag, mag)
+        if qtype == 16:
+            raw = enc.enc_iq2_xxs(d, nib, gidx, sg)
+        elif qtype == 17:
+            raw = enc.enc_iq2_xs(d, nib, gidx, sg)
+        elif qtype == 22:
+            raw = enc.enc_iq2_s(d, nib, gidx, sg)
+        else:
+            raw = enc.enc_iq3_xxs(d, nib, gidx, sg)
+        sc = 1 + 2 * nib  # per 16 (IQ2_XS, IQ2_S) or per 32
+        wd = F32(d) / F32(4.0 if qtype == 18 else 8.0)
+        e = np.arange(256) // (16 if per16 else 32)
+        dq = ((wd * sc[e].astype(F32)) * q.astype(F32)).astype(F32)
+        out.append((raw, q, sc, np.zeros(8, np.int64), wd, F32(0), dq))
+    return out
 
 
 def superblocks(qtype, rng, grid):
     """(raw bytes [n][sb], int quants [n][256], int scales [n][8], int mins [n][8], d [n], dmin [n], dq f32 [n][256])"""
+    if qtype in (16, 17, 18, 22):
+        return iq2_superblocks(qtype, rng)
     out = []
     n_rand = 28
     for i in range(len(D_EDGE) + n_rand):
@@ -162,7 +224,8 @@ def main():
     # per type: edge + random superblocks as an N x K matrix (N = 16 rows of K = 512), its dequantized values,
     # the int32 block sums against the first quantizer row pattern, and the GEMV output
     for qtype, name in ((8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k"), (13, "q5_k"),
-                        (2, "q4_0"), (20, "iq4_nl")):
+                        (2, "q4_0"), (20, "iq4_nl"), (16, "iq2_xxs"), (17, "iq2_xs"), (22, "iq2_s"),
+                        (18, "iq3_xxs")):
         sbs = superblocks(qtype, rng, grid)
         N, K = 16, 512
         nsb = K // 256
@@ -181,7 +244,7 @@ def main():
                     b = 8 * s + j
                     a = aq1[0, 32 * b:32 * b + 32].astype(np.int64)
                     qq = q[32 * j:32 * j + 32].astype(np.int64)
-                    if qtype == 14:  # sc0 * lo + sc1 * hi
+                    if qtype in (14, 17, 22):  # sc0 * lo + sc1 * hi
                         iv = int(sc[2 * j]) * int(np.dot(qq[:16], a[:16])) + int(sc[2 * j + 1]) * int(np.dot(qq[16:], a[16:]))
                     else:
                         iv = int(sc[j]) * int(np.dot(qq, a))

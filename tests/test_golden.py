@@ -1,6 +1,7 @@
 """Known-answer vectors (tests/golden/known_answers.npz, written by tests/golden/make_golden.py from block fields,
 independently of the oracle and the product): the oracle on the CPU, and the HIP path through the C ABI on the GPU.
-Edge cases: d = 0, d = +-65504, subnormal d, all-15 nibbles, IQ3_S grid bit 8 and all sign bits, quantizer ties,
+Edge cases: d = 0, d = +-65504, subnormal d, all-15 nibbles, IQ3_S grid bit 8 and all sign bits, the IQ2 / IQ3_XXS
+last grid index with every stored sign set, quantizer ties,
 zero blocks, +-amax and subnormal inputs."""
 import os
 
@@ -11,7 +12,7 @@ import oracle
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.npz")
 TYPES = [(8, "q8_0"), (12, "q4_k"), (23, "iq4_xs"), (21, "iq3_s"), (14, "q6_k"), (13, "q5_k"), (2, "q4_0"),
-         (20, "iq4_nl")]
+         (20, "iq4_nl"), (16, "iq2_xxs"), (17, "iq2_xs"), (22, "iq2_s"), (18, "iq3_xxs")]
 K = 512
 
 
