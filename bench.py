@@ -168,7 +168,7 @@ def main():
         # dominant kernel: the gate/up matrix (K 5120 -> N 17408)
         gu = per["5120->17408"]
         traffic = profile_traffic("gemv_iq4_xs_5120x17408")
-        out["roofline"] = {"bound": "hbm", "kernel": "gemvs_kernel<IQ4_XS, LPR=32, CH=5> K=5120 N=17408",
+        out["roofline"] = {"bound": "hbm", "kernel": "gemvs_kernel<23, 32, 5, true, 1, 2> (IQ4_XS, 32 lanes per row, 5 blocks per lane, two rows in flight) K=5120 N=17408",
                            "achieved": gu["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gu["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                            "algorithmic_bytes_per_launch": gu["weight_bytes"]}
@@ -206,7 +206,7 @@ def main():
         tops = ops / (ms * 1e-3) / 1e12
         g = {"value": round(tops, 1), "unit": "TOPS", "ms_per_launch": round(ms, 4),
              "config": "Q4_K K=5120 N=17408, M=2048 (1% outlier channels x20), int8 per-32 activations",
-             "roofline": {"bound": "mfma", "kernel": "gemm_kernel<Q4_K, MT=2, dense>", "achieved": round(tops, 1),
+             "roofline": {"bound": "mfma", "kernel": "gemm_kernel<12, 2, 0, false> (Q4_K, 64 x 128 tiles, dense)", "achieved": round(tops, 1),
                           "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                           "traffic": profile_traffic("gemm_q4_k_2048x5120x17408"),
                           "algorithmic_ops_per_launch": int(ops)}}
