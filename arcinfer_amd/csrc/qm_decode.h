@@ -213,6 +213,20 @@ struct BlockInts {
 template <int TYPE>
 __device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1, int mn, const uint4& x0,
                                           const uint4& x1, int bs0, int bs1, int& iv, int& mv) {
+  mv = Traits<TYPE>::MINS ? __mul24(mn, bs0 + bs1) : 0;
+  if constexpr (!Traits<TYPE>::SC16 && !Traits<TYPE>::SPLIT) {
+    // one integer scale per 32-block: a single chain of 8 dot products
+    int sum = dot4(x0.x, wd[0], 0);
+    sum = dot4(x0.y, wd[1], sum);
+    sum = dot4(x0.z, wd[2], sum);
+    sum = dot4(x0.w, wd[3], sum);
+    sum = dot4(x1.x, wd[4], sum);
+    sum = dot4(x1.y, wd[5], sum);
+    sum = dot4(x1.z, wd[6], sum);
+    sum = dot4(x1.w, wd[7], sum);
+    iv = kBlockScales<TYPE> ? sum : __mul24(sc, sum);
+    return;
+  }
   int lo = dot4(x0.x, wd[0], 0);
   lo = dot4(x0.y, wd[1], lo);
   lo = dot4(x0.z, wd[2], lo);
@@ -226,12 +240,7 @@ __device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1,
     iv = __mul24(sc, lo - 32 * bs0) + __mul24(sc1, hi - 32 * bs1);
   } else if constexpr (Traits<TYPE>::SPLIT) {
     iv = __mul24(sc, lo) + __mul24(sc1, hi);
-  } else if constexpr (kBlockScales<TYPE>) {
-    iv = lo + hi;
-  } else {
-    iv = __mul24(sc, lo + hi);
   }
-  mv = Traits<TYPE>::MINS ? __mul24(mn, bs0 + bs1) : 0;
 }
 
 template <int TYPE>

@@ -147,10 +147,12 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s03, uint32_t s47, uint32
   mn = j < 4 ? mn_lo : mn_hi;
 }
 
-// IQ4_XS: the signed scale (ls - 32) of 32-block ib from the header's first two words (src/quants.h:297-312).
+// IQ4_XS: the signed scale ls - 32 of 32-block ib from the prepared header's first two words (src/quants.h:297-312).
+// The prepared header stores scales_h with bit 1 of every 2-bit field flipped, so each field read as a signed 2-bit
+// number is (high bits of ls) - 2, and (field << 4) | (low 4 bits) is ls - 32 in one sign-extending extract.
 __device__ __forceinline__ int iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
-  const int ls = (int)(((h1 >> (4 * ib)) & 0xFu) | (((h0 >> (16 + 2 * ib)) & 3u) << 4));
-  return ls - 32;
+  const int hi = (int)(h0 << (14 - 2 * ib)) >> 30;
+  return (int)((uint32_t)hi << 4 | ((h1 >> (4 * ib)) & 0xFu));
 }
 
 // IQ3_S sign masks: for a sign byte s, m[0]/m[1] = 0xFF in each byte whose sign bit (bits 0..3 / 4..7) is set, and

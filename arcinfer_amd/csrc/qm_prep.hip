@@ -38,8 +38,11 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         q[16 * (2 * j + 1) + t] = (uint8_t)((a >> 4) | ((c >> 4) << 4));
       }
   } else if constexpr (TYPE == T_IQ4_XS) {
-    // d, scales_h, scales_l[4] | qs[128] (block ib = qs[16 ib .. 16 ib + 15], already per-32)
+    // d, scales_h, scales_l[4] | qs[128] (block ib = qs[16 ib .. 16 ib + 15], already per-32); scales_h is stored
+    // with bit 1 of each 2-bit field flipped (0xAAAA), which makes the field a signed (high bits - 2)
     for (int e = 0; e < 8; ++e) h[e] = p[e];
+    h[2] ^= 0xAA;
+    h[3] ^= 0xAA;
     for (int e = 0; e < 128; ++e) q[e] = p[8 + e];
   } else if constexpr (TYPE == T_Q5_K) {
     // d, dmin, scales[12] | qh[32] | qs[128] (src/quants.h:91-114): chunk j's low / high nibbles are blocks 2j / 2j+1,
