@@ -99,7 +99,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
   const int m = blockIdx.x, nb = F / 32, sub = threadIdx.x & 7;
   const bool valid = m < M;
   const float* g = gu + (size_t)m * ldg;
-  for (int b0 = 0; b0 < nb; b0 += 32) {
+  // (grid.y splits the row: no step crosses a 32-block, so chunks of 32 blocks are independent)
+  for (int b0 = 32 * blockIdx.y; b0 < nb; b0 += 32 * gridDim.y) {
     const int b = b0 + (threadIdx.x >> 3);
     const bool live = b < nb;
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -120,6 +121,57 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
   }
 }
 
+// rmsnorm_quant_kernel for K <= 16384 with the row held in registers: work-group (m, c) reads the whole row x once
+// (every load issued up front) for the mean square, then scales and quantizes its passes c, c + gridDim.y, ... of 32
+// blocks (1024 values) each. With few rows the launch splits each row over work-groups (gridDim.y > 1: every one
+// re-reads the row, cheap at decode sizes); with many rows one work-group takes the whole row. Thread t holds elements 1024 p + 4 t .. + 3 of pass p, the elements and order of sumsq_row's loop,
+// so every work-group of a row computes the same, bit-identical r as rmsnorm_quant_kernel.
+template <int PASSES>
+__global__ __launch_bounds__(256) void rmsnorm_quant_reg_kernel(const float* __restrict__ x, int ldx,
+                                                                const float* __restrict__ w, int K, int M,
+                                                                int M_stride, float eps, int8_t* __restrict__ aq,
+                                                                float* __restrict__ asc, int16_t* __restrict__ absum,
+                                                                float* __restrict__ h, int ldh) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, c = blockIdx.y, nb = K / 32, sub = threadIdx.x & 7;
+  const bool valid = m < M;
+  const float* xr = x + (size_t)m * ldx;
+  float4 xv[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int b = 32 * p + (threadIdx.x >> 3);
+    xv[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (b < nb && valid) xv[p] = *(const float4*)(xr + 32 * b + 4 * sub);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    ss = fmaf(xv[p].x, xv[p].x, ss);
+    ss = fmaf(xv[p].y, xv[p].y, ss);
+    ss = fmaf(xv[p].z, xv[p].z, ss);
+    ss = fmaf(xv[p].w, xv[p].w, ss);
+  }
+  ss = block_sum(ss, red);
+  const float r = valid ? 1.0f / sqrtf(ss / (float)K + eps) : 0.0f;
+  // this work-group's passes: c, c + gridDim.y, ... (all of them when the grid does not split rows)
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    if (p % gridDim.y != (unsigned)c) continue;
+    const int b = 32 * p + (threadIdx.x >> 3);
+    const bool live = b < nb;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live && valid) {
+      const float4 wv = *(const float4*)(w + 32 * b + 4 * sub);
+      v[0] = xv[p].x * r * wv.x;
+      v[1] = xv[p].y * r * wv.y;
+      v[2] = xv[p].z * r * wv.z;
+      v[3] = xv[p].w * r * wv.w;
+    }
+    if (h && live) *(float4*)(h + (size_t)m * ldh + 32 * b + 4 * sub) = make_float4(v[0], v[1], v[2], v[3]);
+    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum);
+  }
+}
+
 // x = (x + t * r * w) * s (r from t's mean square), stored back; y = x * r2 * w2 (r2 from the new x) or, without
 // w2, y = x; y quantized (ops.cl:2025-2075). The new x stays in registers between the two steps (PASSES = K / 1024
 // rounded up, at most 16: K <= 16384).
@@ -134,7 +186,30 @@ __global__ __launch_bounds__(256) void add_norm_quant_kernel(float* __restrict__
   const bool valid = m < M;
   float* xr = x + (size_t)m * K;
   const float* tr = t + (size_t)m * K;
-  const float r = valid ? 1.0f / sqrtf(sumsq_row(tr, K, red) / (float)K + eps) : 0.0f;
+  // every load of x, t and w issued up front; thread t holds elements 1024 p + 4 t .. + 3, the order of sumsq_row's
+  // loop, so the mean square of t is bit-identical to a separate pass over t
+  float4 x4s[PASSES], t4s[PASSES], w4s[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int b = 32 * p + (threadIdx.x >> 3);
+    x4s[p] = t4s[p] = w4s[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (b < nb && valid) {
+      const int o = 32 * b + 4 * sub;
+      x4s[p] = *(const float4*)(xr + o);
+      t4s[p] = *(const float4*)(tr + o);
+      w4s[p] = *(const float4*)(w + o);
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    ss = fmaf(t4s[p].x, t4s[p].x, ss);
+    ss = fmaf(t4s[p].y, t4s[p].y, ss);
+    ss = fmaf(t4s[p].z, t4s[p].z, ss);
+    ss = fmaf(t4s[p].w, t4s[p].w, ss);
+  }
+  ss = block_sum(ss, red);
+  const float r = valid ? 1.0f / sqrtf(ss / (float)K + eps) : 0.0f;
   float xv[PASSES][4];
   float s2 = 0.0f;
 #pragma unroll
@@ -144,7 +219,7 @@ __global__ __launch_bounds__(256) void add_norm_quant_kernel(float* __restrict__
     for (int i = 0; i < 4; ++i) xv[p][i] = 0.0f;
     if (b < nb && valid) {
       const int o = 32 * b + 4 * sub;
-      const float4 x4 = *(const float4*)(xr + o), t4 = *(const float4*)(tr + o), w4 = *(const float4*)(w + o);
+      const float4 x4 = x4s[p], t4 = t4s[p], w4 = w4s[p];
       xv[p][0] = (x4.x + t4.x * r * w4.x) * s;
       xv[p][1] = (x4.y + t4.y * r * w4.y) * s;
       xv[p][2] = (x4.z + t4.z * r * w4.z) * s;
@@ -176,13 +251,24 @@ __global__ __launch_bounds__(256) void add_norm_quant_kernel(float* __restrict__
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps,
                                 int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, hipStream_t s) {
-  rmsnorm_quant_kernel<<<M_stride, 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh);
+  const int passes = (K / 32 + 31) / 32;
+  const unsigned split = M_stride < 256 ? (unsigned)passes : 1u;  // (few rows: the GPU would be nearly idle)
+#define QM_RNQ(P) rmsnorm_quant_reg_kernel<P><<<dim3(M_stride, split), 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh)
+  if (passes <= 1) QM_RNQ(1);
+  else if (passes <= 2) QM_RNQ(2);
+  else if (passes <= 4) QM_RNQ(4);
+  else if (passes <= 8) QM_RNQ(8);
+  else if (passes <= 16) QM_RNQ(16);
+  else rmsnorm_quant_kernel<<<M_stride, 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh);
+#undef QM_RNQ
   return hipGetLastError();
 }
 
 hipError_t launch_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
                                float* asc, int16_t* absum, hipStream_t s) {
-  swiglu_quant_kernel<<<M_stride, 256, 0, s>>>(gu, ldg, F, M, M_stride, fused, gelu, aq, asc, absum);
+  // one work-group per row and chunk of 32 blocks (1024 values): a decode row of F = 17408 spreads over 17
+  const unsigned chunks = (unsigned)((F / 32 + 31) / 32);
+  swiglu_quant_kernel<<<dim3(M_stride, chunks), 256, 0, s>>>(gu, ldg, F, M, M_stride, fused, gelu, aq, asc, absum);
   return hipGetLastError();
 }
 

@@ -7,6 +7,8 @@ Metric: IQ4_XS GEMV weight GB/s (decode) + int8 GEMM TOPS (2K pr
   gemm      -- the 2K-token prompt GEMM: Q4_K weights K=5120, N=17408, M=2048 int8 activations, int8 MFMA;
                TOPS = 2*M*N*K / time.
   moe       -- the MoE FFN (256 experts, E 2048, F 512, T 4096, top-8, Zipf 1.1 router, IQ4_XS), reported.
+  reported  -- the other BASELINE configs (Q8_0 4096x4096 GEMV; IQ3_S 5120x5120 GEMV at M=1 and GEMM at M=512)
+               and the activation producers that feed the path (rmsnorm_quant, swiglu_quant, add_norm_quant).
   roofline  -- for each kernel: algorithmic bytes (or int8 ops) per launch / average launch time, measured with
                HIP events on the launch stream, against MI355X peaks (HBM 8 TB/s, dense int8 MFMA 5.0 POPS).
   cpu_baseline -- the repository's C restatement of the reference CPU path (oracle/), timed on this host.
@@ -31,7 +33,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["all", "gemv", "gemm", "moe"], default="all")
+    p.add_argument("--only", choices=["all", "gemv", "gemm", "moe", "report"], default="all")
     p.add_argument("--copies", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU work budget per baseline leg")
@@ -271,6 +273,59 @@ def main():
         out["moe"]["decode"] = dec
         for w_ in ws_:
             w_.release()
+
+    # ---------------- the other BASELINE configs and the activation producers (reported)
+    if args.only in ("all", "report"):
+        rep = {}
+        for name, qtype, N, K, seed in (("q8_0_gemv_4096x4096", F.Q8_0, 4096, 4096, 0),
+                                         ("iq3_s_gemv_5120x5120", F.IQ3_S, 5120, 5120, 3)):
+            W = F.synth_weight(qtype, N, K, seed=seed)
+            Wd = torch.from_numpy(W).to(dev)
+            copies = [qm.QWeight(qtype, Wd, N, K) for _ in range(args.copies)]
+            del Wd
+            x = torch.from_numpy(F.synth_activations(1, K, seed=seed)).to(dev)
+            aq, asc, absum = qm.quantize_act(x, M_stride=16)
+            C = torch.empty((1, N), device=dev)
+            msg = timed_graph(lambda i, copies=copies, aq=aq, asc=asc, absum=absum, C=C, N=N:
+                              qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N), args, stream)
+            b = F.weight_bytes(qtype, N, K)
+            rep[name] = {"us_per_launch": round(msg * 1e3, 2), "weight_GB/s": round(b / (msg * 1e-3) / 1e9, 1),
+                         "frac_of_hbm_peak": round(b / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "weight_bytes": b}
+            if qtype == F.IQ3_S:
+                M = 512
+                xm = torch.from_numpy(F.synth_activations(M, K, seed=seed)).to(dev)
+                aqm, ascm, absm = qm.quantize_act(xm)
+                Cm = torch.empty((M, N), device=dev)
+                msm, _ = timed(lambda i: qm.gemm(copies[0], aqm, ascm, absm, C=Cm, ldc=N), max(2, args.steps // 5),
+                               args.warmup, stream)
+                ops = 2.0 * M * N * K
+                rep["iq3_s_gemm_512x5120x5120"] = {"ms_per_launch": round(msm, 4),
+                                                    "TOPS": round(ops / (msm * 1e-3) / 1e12, 1),
+                                                    "frac_of_int8_peak": round(ops / (msm * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                                                    "ops": int(ops)}
+            for c in copies:
+                c.release()
+        # producers: decode (1 row) and prompt (2048 rows) sizes of the 27B-class shapes; bytes = f32 inputs read +
+        # int8 rows, per-32 scales and per-16 sums written (+ the residual written back for add_norm_quant)
+        K, Fd = 5120, 17408
+        prod = {}
+        for M in (1, 2048):
+            x = torch.randn((M, K), device=dev)
+            wv = torch.randn((K,), device=dev)
+            gu = torch.randn((M, 2 * Fd), device=dev)
+            t = torch.randn((M, K), device=dev)
+            outb = lambda n: n + n // 32 * 4 + n // 16 * 2
+            cases = (("rmsnorm_quant", lambda i: qm.rmsnorm_quant(x, wv, 1e-6), M * (4 * K) + 4 * K + M * outb(K)),
+                     ("swiglu_quant", lambda i: qm.swiglu_quant(gu, Fd, fused=True), M * 8 * Fd + M * outb(Fd)),
+                     ("add_norm_quant", lambda i: qm.add_norm_quant(x, t, wv, 1e-6, 1.0),
+                      M * 12 * K + 4 * K + M * outb(K)))
+            for nm, fn, byts in cases:
+                msp = timed_graph(fn, args, stream) if M == 1 else timed(fn, max(2, args.steps // 5), args.warmup,
+                                                                           stream)[0]
+                prod[f"{nm}_M{M}"] = {"us": round(msp * 1e3, 2), "GB/s": round(byts / (msp * 1e-3) / 1e9, 1)}
+        rep["producers_K5120_F17408"] = prod
+        out["reported"] = rep
+        torch.cuda.empty_cache()
 
     if args.profile:
         # calibration copy for the FETCH_SIZE / WRITE_SIZE counters: 1 GiB read + 1 GiB written

@@ -26,7 +26,7 @@ def near_int8(a, b):
     return d.max() <= 1 and np.mean(d > 0) <= 1e-3
 
 
-@pytest.mark.parametrize("M,Ms,K", [(1, 16, 5120), (7, 8, 2048), (3, 3, 17408), (2, 4, 96)])
+@pytest.mark.parametrize("M,Ms,K", [(1, 16, 5120), (7, 8, 2048), (3, 3, 17408), (2, 4, 96), (300, 304, 2048)])
 def test_rmsnorm_quant(qm, dev, M, Ms, K):
     import torch
     rng = np.random.default_rng(M + K)
@@ -45,7 +45,7 @@ def test_rmsnorm_quant(qm, dev, M, Ms, K):
 
 
 @pytest.mark.parametrize("gelu", [False, True])
-@pytest.mark.parametrize("M,Ms,F", [(1, 16, 17408), (5, 8, 512), (2, 2, 96)])
+@pytest.mark.parametrize("M,Ms,F", [(1, 16, 17408), (5, 8, 512), (2, 2, 96), (260, 260, 1024)])
 def test_swiglu_quant(qm, dev, gelu, M, Ms, F):
     import torch
     rng = np.random.default_rng(F + M)
