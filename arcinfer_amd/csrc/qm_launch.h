@@ -71,9 +71,9 @@ hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, i
 hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
                               hipStream_t s);
 hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s);
-// MoE at decode sizes (qm_moe_dec.hip): gate/up -> h (f32 [T*NU][F]), then down + combine into x
+// MoE at decode sizes (qm_moe_dec.hip): routing + gate/up -> ids, wts, h (f32 [T*NU][F]), then down + combine into x
 hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const WView& down, int T, int NU, int E,
-                             int F, const int* ids, const float* wts, const int8_t* aq, const float* asc, int M_stride,
-                             float* h, float* x, int accumulate, hipStream_t s);
+                             int F, const float* logits, int ldl, int NE, int* ids, float* wts, const int8_t* aq,
+                             const float* asc, int M_stride, float* h, float* x, int accumulate, hipStream_t s);
 
 }  // namespace qm

@@ -2,11 +2,12 @@
 // per expert), scatter (device-side token -> slot permutation) and combine (each token's expert outputs summed in
 // selection order). The expert matrices themselves run in qm_gemm.hip's tile modes.
 #include "qm_launch.h"
+#include "qm_route.h"
 
 namespace qm {
 
 // One wave per token (each wave walks tpw tokens): the top NU of the NE logits by repeated arg-max (ties: the lower
-// expert), weights exp(l - max) / sum over the selection (summed in selection order). Per-expert counts go through
+// expert), weights exp(l - max) / sum over the selection (summed in selection order; route_token). Per-expert counts go through
 // a work-group histogram in LDS and one global atomic per (work-group, expert), not one per (token, k): the router's
 // skew (Zipf) would otherwise serialise thousands of atomics on the popular experts' counters.
 // zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of 16-lane sub-groups.
@@ -22,47 +23,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   for (int j = 0; j < tpw; ++j) {
     const int t = (blockIdx.x * 4 + wave) * tpw + j;
     if (t >= T) break;
-    const float* lg = logits + (size_t)t * ldl;
-    float v[PER_LANE];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) {
-      const int e = i * 64 + lane;
-      v[i] = e < NE ? lg[e] : -INFINITY;
-      mx = fmaxf(mx, v[i]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float sum = 0.0f, my_p = 0.0f;
-    int my_e = 0;
-    for (int k = 0; k < NU; ++k) {
-      float bv = -INFINITY;
-      int bi = NE;
-#pragma unroll
-      for (int i = 0; i < PER_LANE; ++i)
-        if (v[i] > bv) {
-          bv = v[i];
-          bi = i * 64 + lane;
-        }
-      float gv = bv;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
-      int gi = (bv == gv && bi < NE) ? bi : NE;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
-#pragma unroll
-      for (int i = 0; i < PER_LANE; ++i)
-        if (i * 64 + lane == gi) v[i] = -INFINITY;
-      const float p = expf(gv - mx);
-      sum += p;
-      if (lane == k) {
-        my_p = p;
-        my_e = gi;
-      }
-    }
+    int my_e;
+    float my_w;
+    route_token<PER_LANE>(logits + (size_t)t * ldl, NE, NU, lane, my_e, my_w);
     if (lane < NU) {
       ids[(size_t)t * NU + lane] = my_e;
-      wts[(size_t)t * NU + lane] = my_p / sum;
+      wts[(size_t)t * NU + lane] = my_w;
       if (counts) atomicAdd(&hist[my_e], 1);
     }
   }

@@ -3,6 +3,7 @@
 // path: h = up * silu(gate) per expert row, h quantized per 32 (moe.cl:251-282), down times the routing weight, and
 // the token's NU expert outputs summed in selection order (moe.cl:332-340).
 #include "qm_decode.h"
+#include "qm_route.h"
 
 namespace qm {
 
@@ -19,21 +20,50 @@ __device__ __forceinline__ int block_isum(const RawBlk& r, const typename LdsFor
 
 }  // namespace
 
-// Gate/up: grid (slots, F / 8). A work-group stages its token's int8 row in LDS (two 16-byte planes per 32-block, as
-// the decode GEMV) and its 8 lane groups of 32 take one expert row j each: g = gate_e[j] . a_t, u = up_e[j] . a_t,
-// h[slot][j] = u * silu(g). CH = ceil(E / 1024) blocks per lane.
-template <int TYPE, int CH>
-__global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView up, const int* __restrict__ ids, int NU,
-                                                             int F, const int8_t* __restrict__ aq,
+// Gate/up: grid (slots, F / 8), routing included (logits non-null; else ids holds the routing). Wave 0 of every
+// work-group routes the slot's token (route_token:
+// the route kernel's arithmetic, so every work-group of a token selects the same experts) while the work-group stages
+// the token's int8 row in LDS (two 16-byte planes per 32-block, as the decode GEMV); the work-groups with
+// blockIdx.y == 0 of the token's first slot publish ids / wts for the down kernel. Then its 8 lane groups of 32 take
+// one expert row j each: g = gate_e[j] . a_t, u = up_e[j] . a_t, h[slot][j] = u * silu(g). CH = ceil(E / 1024) blocks
+// per lane.
+template <int TYPE, int CH, int PER_LANE>
+__global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView up, const float* __restrict__ logits,
+                                                             int ldl, int NE, int* __restrict__ ids,
+                                                             float* __restrict__ wts, int NU, int F,
+                                                             const int8_t* __restrict__ aq,
                                                              const float* __restrict__ asc, int M_stride,
                                                              float* __restrict__ h) {
   extern __shared__ uint4 smem[];
   __shared__ typename LdsFor<TYPE>::type lds;
+  __shared__ int sel[64];
   using Tr = Traits<TYPE>;
   const int E = gate.K, nb = E / 32;
   uint8_t* sq = (uint8_t*)smem;
   float* ssc = (float*)(sq + (size_t)E);
-  const int slot = blockIdx.x, t = slot / NU, e = ids[slot];
+  const int slot = blockIdx.x, t = slot / NU, k = slot % NU;
+  if (threadIdx.x < 64 && !logits) {
+    if (threadIdx.x < NU) sel[threadIdx.x] = ids[(size_t)t * NU + threadIdx.x];  // (routed by a separate launch)
+  } else if (threadIdx.x < 64) {
+    int my_e;
+    float my_w;
+    route_token<PER_LANE>(logits + (size_t)t * ldl, NE, NU, threadIdx.x, my_e, my_w);
+    if (threadIdx.x < NU) {
+      sel[threadIdx.x] = my_e;
+      if (blockIdx.y == 0 && k == 0) {
+        ids[(size_t)t * NU + threadIdx.x] = my_e;
+        wts[(size_t)t * NU + threadIdx.x] = my_w;
+      }
+    }
+  }
+  lds_fill<TYPE>(&lds);
+  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
+    const int b = i >> 1, hh = i & 1;
+    *(uint4*)(sq + (size_t)hh * nb * 16 + b * 16) = *(const uint4*)(aq + (size_t)t * E + 32 * b + 16 * hh);
+  }
+  for (int b = threadIdx.x; b < nb; b += 256) ssc[b] = asc[(size_t)b * M_stride + t];
+  __syncthreads();
+  const int e = sel[k];
   const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
   const int j = min((int)blockIdx.y * 8 + grp, F - 1);
   const size_t row = (size_t)e * F + j;
@@ -44,13 +74,6 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
     rg[u] = load_block_at<TYPE>(gate.qs + row * nb * Tr::QB, gate.hdr + row * (nb / 8) * Tr::HB, b);
     ru[u] = load_block_at<TYPE>(up.qs + row * nb * Tr::QB, up.hdr + row * (nb / 8) * Tr::HB, b);
   }
-  lds_fill<TYPE>(&lds);
-  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
-    const int b = i >> 1, hh = i & 1;
-    *(uint4*)(sq + (size_t)hh * nb * 16 + b * 16) = *(const uint4*)(aq + (size_t)t * E + 32 * b + 16 * hh);
-  }
-  for (int b = threadIdx.x; b < nb; b += 256) ssc[b] = asc[(size_t)b * M_stride + t];
-  __syncthreads();
   const KvTab kv = kv_tab();
   float g = 0.0f, uu = 0.0f;
 #pragma unroll
@@ -150,20 +173,38 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
   }
 }
 
+template <int TYPE, int PL>
+static void gateup_dec(const dim3& gg, size_t shg, int nbE, const WView& gate, const WView& up, const float* logits,
+                       int ldl, int NE, int* ids, float* wts, int NU, int F, const int8_t* aq, const float* asc,
+                       int M_stride, float* h, hipStream_t s) {
+#define QM_GUD(CH) \
+  moe_gateup_dec_kernel<TYPE, CH, PL><<<gg, 256, shg, s>>>(gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h)
+  switch ((nbE + 31) / 32) {
+    case 1: QM_GUD(1); break;
+    case 2: QM_GUD(2); break;
+    case 3:
+    case 4: QM_GUD(4); break;
+    default: QM_GUD(8); break;
+  }
+#undef QM_GUD
+}
+
 template <int TYPE>
 static hipError_t moe_dec_typed(const WView& gate, const WView& up, const WView& down, int T, int NU, int E, int F,
-                                const int* ids, const float* wts, const int8_t* aq, const float* asc, int M_stride,
-                                float* h, float* x, int accumulate, hipStream_t s) {
+                                const float* logits, int ldl, int NE, int* ids, float* wts, const int8_t* aq,
+                                const float* asc, int M_stride, float* h, float* x, int accumulate, hipStream_t s) {
   const int slots = T * NU, nbE = E / 32, nbF = F / 32;
   const size_t shg = (size_t)E + sizeof(float) * nbE;
   const dim3 gg((unsigned)slots, (unsigned)((F + 7) / 8));
-  switch ((nbE + 31) / 32) {
-    case 1: moe_gateup_dec_kernel<TYPE, 1><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
-    case 2: moe_gateup_dec_kernel<TYPE, 2><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
-    case 3:
-    case 4: moe_gateup_dec_kernel<TYPE, 4><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
-    default: moe_gateup_dec_kernel<TYPE, 8><<<gg, 256, shg, s>>>(gate, up, ids, NU, F, aq, asc, M_stride, h); break;
+  if (T > 4) {
+    // (more tokens: every gate/up work-group routing its token in front of its weight loads costs more than a
+    //  separate route launch; measured at T = 8)
+    const hipError_t e = launch_moe_route(logits, ldl, T, NE, NU, ids, wts, nullptr, s);
+    if (e != hipSuccess) return e;
+    logits = nullptr;
   }
+  if (NE <= 256) gateup_dec<TYPE, 4>(gg, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
+  else gateup_dec<TYPE, 16>(gg, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t shd = (size_t)NU * F + sizeof(float) * NU * nbF;
@@ -180,16 +221,16 @@ static hipError_t moe_dec_typed(const WView& gate, const WView& up, const WView&
 }
 
 hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const WView& down, int T, int NU, int E,
-                             int F, const int* ids, const float* wts, const int8_t* aq, const float* asc, int M_stride,
-                             float* h, float* x, int accumulate, hipStream_t s) {
+                             int F, const float* logits, int ldl, int NE, int* ids, float* wts, const int8_t* aq,
+                             const float* asc, int M_stride, float* h, float* x, int accumulate, hipStream_t s) {
   switch (type) {
-    case T_Q8_0: return moe_dec_typed<T_Q8_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_IQ4_XS: return moe_dec_typed<T_IQ4_XS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_IQ3_S: return moe_dec_typed<T_IQ3_S>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_Q4_0: return moe_dec_typed<T_Q4_0>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_IQ4_NL: return moe_dec_typed<T_IQ4_NL>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_IQ2_XXS: return moe_dec_typed<T_IQ2_XXS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
-    case T_IQ3_XXS: return moe_dec_typed<T_IQ3_XXS>(gate, up, down, T, NU, E, F, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_Q8_0: return moe_dec_typed<T_Q8_0>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ4_XS: return moe_dec_typed<T_IQ4_XS>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ3_S: return moe_dec_typed<T_IQ3_S>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_Q4_0: return moe_dec_typed<T_Q4_0>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ4_NL: return moe_dec_typed<T_IQ4_NL>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ2_XXS: return moe_dec_typed<T_IQ2_XXS>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
+    case T_IQ3_XXS: return moe_dec_typed<T_IQ3_XXS>(gate, up, down, T, NU, E, F, logits, ldl, NE, ids, wts, aq, asc, M_stride, h, x, accumulate, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,0 +1,55 @@
+// Top-k routing of one token by one 64-lane wave: softmax over the selected experts of a row of router logits.
+// Selection takes the largest logit NU times (ties to the lower expert), the weights are exp(l - max) / sum over the
+// selection (summed in selection order). zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of
+// 16-lane sub-groups. Used by route_kernel (qm_moe.hip) and, at decode sizes, inside the expert gate/up kernel.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+namespace qm {
+
+// lg: the token's NE logits; lane < NU receives the k = lane-th selected expert and its weight
+template <int PER_LANE>
+__device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE, int NU, int lane, int& my_e,
+                                            float& my_w) {
+  float v[PER_LANE];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    const int e = i * 64 + lane;
+    v[i] = e < NE ? lg[e] : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float sum = 0.0f, my_p = 0.0f;
+  my_e = 0;
+  for (int k = 0; k < NU; ++k) {
+    float bv = -INFINITY;
+    int bi = NE;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i)
+      if (v[i] > bv) {
+        bv = v[i];
+        bi = i * 64 + lane;
+      }
+    float gv = bv;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
+    int gi = (bv == gv && bi < NE) ? bi : NE;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i)
+      if (i * 64 + lane == gi) v[i] = -INFINITY;
+    const float p = expf(gv - mx);
+    sum += p;
+    if (lane == k) {
+      my_p = p;
+      my_e = gi;
+    }
+  }
+  my_w = my_p / sum;
+}
+
+}  // namespace qm

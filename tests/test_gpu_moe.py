@@ -115,7 +115,8 @@ def test_moe_baseline_config_token_sample(qm, dev):
 @pytest.mark.parametrize("qtype,NE,E,Fd,T,NU", [(F.IQ4_XS, 256, 2048, 512, 1, 8), (F.IQ4_XS, 256, 2048, 512, 8, 8),
                                                 (F.IQ3_S, 16, 1024, 1024, 3, 4), (F.Q8_0, 8, 512, 2048, 2, 2),
                                                 (F.Q4_0, 8, 512, 512, 4, 2), (F.IQ4_NL, 16, 512, 256, 2, 4),
-                                                (F.IQ2_XXS, 16, 1024, 512, 3, 4), (F.IQ3_XXS, 8, 512, 1024, 2, 2)])
+                                                (F.IQ2_XXS, 16, 1024, 512, 3, 4), (F.IQ3_XXS, 8, 512, 1024, 2, 2),
+                                                (F.IQ4_XS, 300, 256, 256, 2, 4)])
 def test_moe_decode_sizes_match_oracle(qm, dev, qtype, NE, E, Fd, T, NU):
     """T * NU <= 64: the GEMV-shaped decode kernels (gate/up -> h -> down + combine in k order)."""
     import torch
