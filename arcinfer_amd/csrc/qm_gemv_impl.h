@@ -314,10 +314,27 @@ static size_t gemvs_lds(int type, int K, int TB) {
 template <int TYPE, int LPR, int CH, bool EXACT, int TB>
 static hipError_t gos(const GemvArgs& a, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
-  // two work-groups per CU (256 CUs), fewer when the matrix has fewer rows than lane groups
-  const int wgs = min(512, (a.w.rows + GPW - 1) / GPW);
-  // batch 1: two rows in flight per lane group; with more tokens the registers go to the token rows
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, TB == 1 ? 2 : 1><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
+  constexpr int PF = TB == 1 ? 2 : 1;  // batch 1: two rows in flight per lane group; more tokens: registers to tokens
+  // Persistent grid: two work-groups per CU, or as many as the kernel's registers and LDS let reside (the 8-token
+  // instantiation needs more than 256 registers: one wave per SIMD), so the whole grid is resident at once; fewer
+  // when the matrix has fewer rows than lane groups. Occupancy is queried once, for this instantiation's largest K.
+  static const int per_cu = [] {
+    int n = 0;
+    const size_t lds_max = gemvs_lds(TYPE, 32 * LPR * CH, TB);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF>, 256, lds_max) !=
+            hipSuccess || n < 1)
+      n = 1;
+    return min(2, n);
+  }();
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1)
+      n = 256;
+    return n;
+  }();
+  const int wgs = min(per_cu * cus, (a.w.rows + GPW - 1) / GPW);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
 
