@@ -112,8 +112,8 @@ def test_gemv_accumulate_offset_and_tokens(qm, dev, qtype):
            for t in range(4)]
     multi = qm.gemv(w, aq, asc, absum, T=4)
     torch.cuda.synchronize()
-    for t in range(4):  # same lanes, same order per token: bit-identical
-        assert torch.equal(one[t][0], multi[t])
+    for t in range(4):  # (T > 2 runs on the MFMA kernel: another f32 summation order than T = 1)
+        assert rel_err(multi[t].cpu().numpy(), one[t][0].cpu().numpy()) < 1e-5
     C = torch.full((4, 3 * N), 2.0, device=dev)
     qm.gemv(w, aq, asc, absum, T=4, C=C, ldc=3 * N, c_off=N, accumulate=1)
     torch.cuda.synchronize()
