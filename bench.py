@@ -225,6 +225,23 @@ def main():
             g["cpu_baseline"] = {"value": round(ops / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthreads,
                                  "kind": "port", "sample": f"every {stride}th output column of the same GEMM "
                                                            f"(oracle/qref.c int8 block-dot), time x {stride}"}
+            # the other two CPU paths of the reference: the activation quantizer (quantize_act_cpu, one thread)
+            # and the f32 dequantize-and-multiply reference (tools/ref_forward.cpp matmul: dequant_row + dot)
+            xh = x.cpu().numpy()
+            t0 = time.perf_counter()
+            oracle.quantize_act(xh)
+            q_s = time.perf_counter() - t0
+            Ms_ = 64
+            t0 = time.perf_counter()
+            oracle.matmul_f32(F.Q4_K, W, K, xh[:Ms_], nthreads=nthreads)
+            f_s = time.perf_counter() - t0
+            g["cpu_baseline_other_paths"] = {
+                "quantize_act": {"us": round(q_s * 1e6, 1), "cores": 1, "kind": "port",
+                                 "sample": "the same 2048 x 5120 f32 activations (oracle/qref.c)",
+                                 "gpu_us": g["quantize_us"]},
+                "matmul_f32": {"value": round(2.0 * Ms_ * N * K / f_s / 1e12, 5), "unit": "TFLOP/s", "cores": nthreads,
+                               "kind": "port",
+                               "sample": f"the first {Ms_} tokens of the same GEMM, f32 dequantized weights, f64 dots"}}
         # the same prompt GEMM with Q6_K weights (per-16 scales: two K=16 MFMAs per block), reported
         W6 = F.synth_weight(F.Q6_K, N, K, seed=6)
         w6 = qm.QWeight(F.Q6_K, torch.from_numpy(W6).to(dev), N, K)
