@@ -2,6 +2,8 @@
 // truncated or hostile file yields an error message, never an out-of-range read.
 #include "qm_gguf.h"
 
+#include <cstdio>
+
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -112,7 +114,45 @@ std::unique_ptr<Gguf> Gguf::open(const std::string& path, std::string& err) {
   }
   g->base_ = (const uint8_t*)m;
   if (!g->parse(err)) return nullptr;
+  if (!g->open_parts(path, err)) return nullptr;
   return g;
+}
+
+// name-00001-of-0000N.gguf with split.count = N > 1: parts 2..N (same name, part number in the same 5 digits), their
+// tensors appended unless a name is already indexed (src/gguf.h:170-187). A part that is missing or malformed fails
+// the open.
+bool Gguf::open_parts(const std::string& path, std::string& err) {
+  const auto it = kv.find("split.count");
+  if (it == kv.end() || it->second.type == GV_STR || it->second.type == GV_ARR || it->second.type == GV_F32 ||
+      it->second.type == GV_F64)
+    return true;
+  const int64_t n = it->second.i;
+  if (n <= 1) return true;
+  const size_t at = path.rfind("-00001-of-");
+  if (at == std::string::npos) return true;  // (a later part opened on its own: only its own tensors)
+  if (n > 99999) {
+    err = "split.count " + std::to_string(n) + " out of range";
+    return false;
+  }
+  for (int64_t k = 2; k <= n; ++k) {
+    char num[8];
+    snprintf(num, sizeof num, "%05d", (int)k);
+    std::string pp = path;
+    pp.replace(at + 1, 5, num);
+    std::string perr;
+    std::unique_ptr<Gguf> part = open(pp, perr);
+    if (!part) {
+      err = "split part " + std::to_string(k) + " of " + std::to_string(n) + ": " + perr;
+      return false;
+    }
+    for (const GgufTensorInfo& t : part->tensors) {
+      if (index.count(t.name)) continue;
+      index[t.name] = tensors.size();
+      tensors.push_back(t);
+    }
+    parts_.push_back(std::move(part));
+  }
+  return true;
 }
 
 Gguf::~Gguf() {

@@ -1,7 +1,9 @@
 // GGUF (v2/v3) reader, host side: maps the file read-only and indexes its metadata and tensor table, so tensors can
 // be handed to qmatmul_prepare_weight straight from the mapping. Follows the published GGUF layout (magic "GGUF",
 // version, tensor count, key-value count, key-values, tensor infos, data aligned to general.alignment); the role of
-// the reference's src/gguf.h:85-305, with POSIX mmap in place of its Win32 mapping and without split-model parts.
+// the reference's src/gguf.h:85-305, with POSIX mmap in place of its Win32 mapping. A split model
+// (name-00001-of-0000N.gguf, "split.count" > 1) opened from its first part maps the other parts too and adds their
+// tensors (src/gguf.h:170-187); a later part opened on its own has only its own tensors.
 #pragma once
 #include <cstdint>
 #include <memory>
@@ -49,6 +51,8 @@ class Gguf {
  private:
   Gguf() = default;
   bool parse(std::string& err);
+  bool open_parts(const std::string& path, std::string& err);
+  std::vector<std::unique_ptr<Gguf>> parts_;  // the other parts of a split model (their mappings stay open)
   const uint8_t* base_ = nullptr;
   uint64_t size_ = 0;
   int fd_ = -1;

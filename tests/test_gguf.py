@@ -52,6 +52,31 @@ def test_gguf_metadata_and_tensors(qm, tmp_path, alignment):
             g.tensor("missing.weight")
 
 
+def test_gguf_split_model(qm, tmp_path):
+    """name-00001-of-0000N.gguf opened from part 1 indexes every part's tensors (src/gguf.h:170-187); a name already
+    indexed keeps its first part's data; a later part opened alone has only its own tensors; a missing part fails."""
+    W1 = F.synth_weight(F.IQ4_XS, 32, 256, seed=3)
+    W2 = F.synth_weight(F.Q8_0, 16, 256, seed=4)
+    W3 = F.synth_weight(F.IQ4_XS, 32, 256, seed=5)
+    part = os.path.join(str(tmp_path), "model-{:05d}-of-00003.gguf")
+    split = lambda k: [("split.no", gw.U16, k), ("split.count", gw.U16, 3)]
+    gw.write_gguf(part.format(1), [("general.architecture", gw.STR, "qwen35")] + split(0),
+                  [("a.weight", F.IQ4_XS, [256, 32], W1.tobytes())])
+    gw.write_gguf(part.format(2), split(1), [("b.weight", F.Q8_0, [256, 16], W2.tobytes()),
+                                             ("a.weight", F.IQ4_XS, [256, 32], W3.tobytes())])
+    gw.write_gguf(part.format(3), split(2), [("c.weight", F.IQ4_XS, [256, 32], W3.tobytes())])
+    with qm.GgufFile(part.format(1)) as g:
+        assert len(g) == 3 and g.get_int("split.count") == 3
+        assert np.array_equal(g.tensor("a.weight").numpy(), W1.ravel())
+        assert np.array_equal(g.tensor("b.weight").numpy(), W2.ravel())
+        assert np.array_equal(g.tensor("c.weight").numpy(), W3.ravel())
+    with qm.GgufFile(part.format(2)) as g:
+        assert len(g) == 2 and np.array_equal(g.tensor("a.weight").numpy(), W3.ravel())
+    os.remove(part.format(3))
+    with pytest.raises(qm.QMatmulError, match="split part 3"):
+        qm.GgufFile(part.format(1))
+
+
 def test_gguf_rejects_malformed_files(qm, tmp_path):
     p, *_ = _sample(tmp_path)
     data = open(p, "rb").read()
