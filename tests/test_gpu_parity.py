@@ -82,7 +82,8 @@ def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
 
 
 @pytest.mark.parametrize("qtype", GEMV_TYPES)
-@pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (200, 2048, 1), (72, 17408, 1), (96, 5120, 2), (64, 1536, 5)])
+@pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (200, 2048, 1), (72, 17408, 1), (96, 5120, 2), (64, 1536, 5),
+                                   (64, 34816, 1), (24, 33024, 3)])  # (K > 32768: the generic kernel)
 def test_gemv_f32_parity(qm, dev, qtype, N, K, T):
     import torch
     rng = np.random.default_rng(qtype * 3 + N)
