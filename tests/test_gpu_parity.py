@@ -167,7 +167,7 @@ def test_gemm_blocksums_bit_exact(qm, dev, qtype, M, N, K):
 
 @pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("M,Ms,N,K", [(64, 64, 256, 1024), (100, 128, 384, 2048), (16, 16, 128, 256),
-                                      (130, 130, 512, 5120)])
+                                      (130, 130, 512, 5120), (96, 96, 128, 17408)])
 def test_gemm_f32_parity(qm, dev, qtype, M, Ms, N, K):
     import torch
     W = F.synth_weight(qtype, N, K, seed=qtype + M + N)
