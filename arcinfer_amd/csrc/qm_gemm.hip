@@ -316,6 +316,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     int isc[8], isc2[8];
     sb_scales<TYPE>(hdr, pay, dsc, dmn, isc);
     if constexpr (GU) sb_scales<TYPE>(hdr2, pay2, dsc2, dmn2, isc2);
+    // each lane carries block 2p + hf's scales into pair p's f32 outer products: picked once per superblock, so only
+    // the lane's four blocks stay live (a bit select, not hf ? x[2p+1] : x[2p]: the compiler turns that into a
+    // lane-dependent index into the array, which it then keeps in scratch memory)
+    float my_dsc4[4], my_dmn4[4], my_dsc24[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      my_dsc4[p] = lane_pick(hfm, dsc[2 * p], dsc[2 * p + 1]);
+      my_dmn4[p] = -lane_pick(hfm, dmn[2 * p], dmn[2 * p + 1]);
+      my_dsc24[p] = GU ? lane_pick(hfm, dsc2[2 * p], dsc2[2 * p + 1]) : 0.0f;
+    }
     const uint4 hcur = hdr, hcur2 = hdr2;
     hdr = load_header<TYPE>(a.w, n, sn);
     if constexpr (GU) hdr2 = load_header<TYPE>(a.w2, n, sn);
@@ -326,11 +336,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       // that buffer's last readers passed the barrier that ended the previous superblock)
       if (p == 2) QM_STORE_ACTS(cur ^ 1)
       // blocks 2p and 2p+1: lanes of k-half hf carry block 2p+hf's scales into the f32 outer-product MFMAs
-      // (a bit select, not hf ? x[2p+1] : x[2p]: the compiler turns that into a lane-dependent index into the
-      //  array, which it then keeps in scratch memory)
-      const float my_dsc = lane_pick(hfm, dsc[2 * p], dsc[2 * p + 1]);
-      const float my_dmn = -lane_pick(hfm, dmn[2 * p], dmn[2 * p + 1]);
-      const float my_dsc2 = GU ? lane_pick(hfm, dsc2[2 * p], dsc2[2 * p + 1]) : 0.0f;
+      const float my_dsc = my_dsc4[p], my_dmn = my_dmn4[p], my_dsc2 = my_dsc24[p];
       v4i bop[2], bop2[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
