@@ -305,6 +305,12 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   }
 }
 
+// Most tokens per gemvs_kernel launch: 8, or 4 where eight tokens' registers would spill (more than 5 blocks per lane,
+// more than 4 for Q6_K) or where two 4-token launches measured faster (IQ2_XXS at 4+ blocks per lane, applied to the
+// grid-decoded types alike); more tokens run as chunks.
+template <int TYPE>
+constexpr int gemvs_max_tb(int ch) { return ch <= (TYPE == T_Q6_K ? 4 : kIq2<TYPE> ? 3 : 5) ? 8 : 4; }
+
 // LDS bytes of gemvs_kernel for TB tokens
 static size_t gemvs_lds(int type, int K, int TB) {
   const int nb = K / 32;
@@ -344,7 +350,9 @@ static hipError_t gos_tb(const GemvArgs& a, hipStream_t s) {
     case 1: return gos<TYPE, LPR, CH, EXACT, 1>(a, s);
     case 2: return gos<TYPE, LPR, CH, EXACT, 2>(a, s);
     case 4: return gos<TYPE, LPR, CH, EXACT, 4>(a, s);
-    default: return gos<TYPE, LPR, CH, EXACT, 8>(a, s);
+    default:
+      if constexpr (gemvs_max_tb<TYPE>(CH) >= 8) return gos<TYPE, LPR, CH, EXACT, 8>(a, s);
+      else return hipErrorInvalidValue;  // (the dispatcher never asks: it chunks by gemvs_max_tb)
   }
 }
 
@@ -385,7 +393,7 @@ hipError_t gemv_dispatch(const GemvArgs& a, hipStream_t s) {
   if (sweep && nb <= 1024) {
     // tokens per launch: as many as fit in 80 KB of LDS (two work-groups per CU), up to 8; more tokens -> chunks
     // of tokens, each launch reading the weights once
-    int tb = 8;
+    int tb = gemvs_max_tb<TYPE>(nb <= 256 ? (nb + 31) / 32 : (nb + 127) / 128);
     const size_t cap = 80 * 1024 - sizeof(typename LdsFor<TYPE>::type);  // (the codebook tables' static LDS)
     while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > cap) tb >>= 1;
     if (gemvs_lds(TYPE, a.w.K, tb) <= cap) {
