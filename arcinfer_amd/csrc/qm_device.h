@@ -270,10 +270,60 @@ __device__ __forceinline__ void iq_group(const IqLds<TYPE>* t, uint32_t p0, uint
 // Per-type scale unit: IQ2 d / 8, IQ3_XXS d / 4 (src/quants.h:172, 222) -- exact powers of two
 template <int TYPE> constexpr float kIqDScale = TYPE == T_IQ3_XXS ? 0.25f : 0.125f;
 
-// ---- wave-level reductions (wave64)
+// ---- cross-lane operations (wave64). Lane moves within a 16-lane row are DPP operands of the VALU op itself; the
+// four rows are combined through v_readlane. (__shfl_xor would be an LDS round trip, ds_bpermute, per step.) Every
+// lane of the wave must be active.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane 7 - i of its 8-lane half-row: the other quad of the 8 lanes
+constexpr int kDppMirror = 0x140;      // lane 15 - i of its row: the other 8 lanes of the row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// max over the 8-lane group holding the lane (every lane of the group receives it)
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+// sum over the 4-lane quad holding the lane (exact for ints)
+__device__ __forceinline__ int sum4_i(int v) {
+  v += dpp_i<kDppXor1>(v);
+  return v + dpp_i<kDppXor2>(v);
+}
+
+// Sum over the aligned group of `width` lanes (2..64, a power of two, known at compile time at every call site).
+// Lane 0 of each group receives the sum; the other lanes of a group of <= 16 receive the same value summed in another
+// order, and every lane of a 32- or 64-lane group receives lane 0's value.
 __device__ __forceinline__ float wave_sum_width(float v, int width) {
-  for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f<kDppXor1>(v);
+  if (width == 2) return v;
+  v += dpp_f<kDppXor2>(v);
+  if (width == 4) return v;
+  v += dpp_f<kDppHalfMirror>(v);
+  if (width == 8) return v;
+  v += dpp_f<kDppMirror>(v);
+  if (width == 16) return v;
+  const float r0 = readlane_f(v, 0), r1 = readlane_f(v, 16), r2 = readlane_f(v, 32), r3 = readlane_f(v, 48);
+  if (width == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+  return (r0 + r1) + (r2 + r3);
+}
+
+// max over the wave; every lane receives it
+__device__ __forceinline__ float wave_max(float v) {
+  v = max8(v);
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 }  // namespace qm

@@ -135,9 +135,7 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
       v[3] = hv.w;
     }
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = max8(amax);
     const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
     uint32_t pk = 0;
 #pragma unroll

@@ -192,9 +192,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     for (int i = 0; i < 4; ++i) v[i] = src[i];
   }
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  amax = max8(amax);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int sum = 0;
   uint32_t pk = 0;
@@ -204,8 +202,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     sum += q;
     pk |= (uint32_t)(q & 0xFF) << (8 * i);
   }
-  sum += __shfl_xor(sum, 1, 64);
-  sum += __shfl_xor(sum, 2, 64);
+  sum = sum4_i(sum);
   if (!live) return;
   *(uint32_t*)(aq + (size_t)m * K + 32 * b + 4 * sub) = pk;
   if (sub == 0) asc[(size_t)b * M_stride + m] = amax / 127.0f;

@@ -14,9 +14,7 @@ __device__ __forceinline__ void quant8(const float v[4], int sub, bool store, in
                                        int8_t* __restrict__ aq, float* __restrict__ asc,
                                        int16_t* __restrict__ absum) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  amax = max8(amax);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int sum = 0;
   uint32_t pk = 0;
@@ -26,18 +24,16 @@ __device__ __forceinline__ void quant8(const float v[4], int sub, bool store, in
     sum += q;
     pk |= (uint32_t)(q & 0xFF) << (8 * i);
   }
-  sum += __shfl_xor(sum, 1, 64);
-  sum += __shfl_xor(sum, 2, 64);
+  sum = sum4_i(sum);
   if (!store) return;
   *(uint32_t*)(aq + (size_t)m * K + 32 * b + 4 * sub) = pk;
   if (sub == 0) asc[(size_t)b * M_stride + m] = amax / 127.0f;
   if ((sub & 3) == 0) absum[(size_t)(2 * b + (sub >> 2)) * M_stride + m] = (int16_t)sum;
 }
 
-// Sum over the work-group's 256 threads, in a fixed order (wave butterflies, then the 4 wave sums in order).
+// Sum over the work-group's 256 threads, in a fixed order (wave sums, then the 4 wave sums in order).
 __device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum_width(v, 64);
   __syncthreads();  // (red may still be read from a previous call)
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();

@@ -1,10 +1,12 @@
 // Top-k routing of one token by one 64-lane wave: softmax over the selected experts of a row of router logits.
 // Selection takes the largest logit NU times (ties to the lower expert), the weights are exp(l - max) / sum over the
 // selection (summed in selection order). zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of
-// 16-lane sub-groups. Used by route_kernel (qm_moe.hip) and, at decode sizes, inside the expert gate/up kernel.
+// 16-lane sub-groups: the wave maximum on DPP / v_readlane, the arg-max by ballot. Used by route_kernel (qm_moe.hip)
+// and, at decode sizes, inside the expert gate/up kernel.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include "qm_device.h"
 
 namespace qm {
 
@@ -20,25 +22,24 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE
     v[i] = e < NE ? lg[e] : -INFINITY;
     mx = fmaxf(mx, v[i]);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = wave_max(mx);
   float sum = 0.0f, my_p = 0.0f;
   my_e = 0;
   for (int k = 0; k < NU; ++k) {
     float bv = -INFINITY;
-    int bi = NE;
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i)
-      if (v[i] > bv) {
-        bv = v[i];
-        bi = i * 64 + lane;
+    for (int i = 0; i < PER_LANE; ++i) bv = fmaxf(bv, v[i]);
+    const float gv = wave_max(bv);
+    // the lowest expert index holding the maximum: the first slice i (experts 64 i .. 64 i + 63) with a match, its
+    // lowest lane; a maximum of -inf (or no finite logit left) selects nothing, gi = NE
+    int gi = NE;
+    if (gv > -INFINITY) {
+#pragma unroll
+      for (int i = PER_LANE - 1; i >= 0; --i) {
+        const unsigned long long m = __ballot(v[i] == gv);
+        if (m) gi = i * 64 + __builtin_ctzll(m);
       }
-    float gv = bv;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) gv = fmaxf(gv, __shfl_xor(gv, o, 64));
-    int gi = (bv == gv && bi < NE) ? bi : NE;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) gi = min(gi, __shfl_xor(gi, o, 64));
+    }
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i)
       if (i * 64 + lane == gi) v[i] = -INFINITY;
