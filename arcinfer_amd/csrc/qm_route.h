@@ -1,8 +1,8 @@
 // Top-k routing of one token by one 64-lane wave: softmax over the selected experts of a row of router logits.
-// Selection takes the largest logit NU times (ties to the lower expert), the weights are exp(l - max) / sum over the
-// selection (summed in selection order). zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of
-// 16-lane sub-groups: the wave maximum on DPP / v_readlane, the arg-max by ballot. Used by route_kernel (qm_moe.hip)
-// and, at decode sizes, inside the expert gate/up kernel.
+// Selection takes the largest logit NU times (ties to the lower expert; -inf logits in expert order), the weights
+// are exp(l - max) / sum over the selection (summed in selection order). zero/kernels/moe.cl:42-81 (moe_route), with
+// 64-lane waves instead of 16-lane sub-groups: the wave maximum on DPP / v_readlane, the arg-max by ballot. Used by
+// route_kernel (qm_moe.hip) and, at decode sizes, inside the expert gate/up kernel.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -24,6 +24,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE
   }
   mx = wave_max(mx);
   float sum = 0.0f, my_p = 0.0f;
+  unsigned taken = 0;  // bit i: expert i * 64 + lane selected
   my_e = 0;
   for (int k = 0; k < NU; ++k) {
     float bv = -INFINITY;
@@ -31,18 +32,21 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE
     for (int i = 0; i < PER_LANE; ++i) bv = fmaxf(bv, v[i]);
     const float gv = wave_max(bv);
     // the lowest expert index holding the maximum: the first slice i (experts 64 i .. 64 i + 63) with a match, its
-    // lowest lane; a maximum of -inf (or no finite logit left) selects nothing, gi = NE
+    // lowest lane. With no finite logit left, the lowest expert not yet selected (a stable sort's order, as the
+    // reference's route test; its OpenCL kernel would yield the out-of-range index NE there). NU <= NE.
     int gi = NE;
-    if (gv > -INFINITY) {
 #pragma unroll
-      for (int i = PER_LANE - 1; i >= 0; --i) {
-        const unsigned long long m = __ballot(v[i] == gv);
-        if (m) gi = i * 64 + __builtin_ctzll(m);
-      }
+    for (int i = PER_LANE - 1; i >= 0; --i) {
+      const bool cand = gv > -INFINITY ? v[i] == gv : !((taken >> i) & 1u) && i * 64 + lane < NE;
+      const unsigned long long m = __ballot(cand);
+      if (m) gi = i * 64 + __builtin_ctzll(m);
     }
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i)
-      if (i * 64 + lane == gi) v[i] = -INFINITY;
+      if (i * 64 + lane == gi) {
+        v[i] = -INFINITY;
+        taken |= 1u << i;
+      }
     const float p = expf(gv - mx);
     sum += p;
     if (lane == k) {
