@@ -121,28 +121,33 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
                                       min(gl + LPR * u, nb - 1));
     }
   lds_fill<TYPE>(&lds);
-  // h rows of the token's NU slots, quantized per 32 (8 lanes per block: the quantizer's arithmetic)
-  for (int b0 = 0; b0 < NU * nb; b0 += 32) {
-    const int bi = b0 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
-    const bool live = bi < NU * nb;
-    const int k = live ? bi / nb : 0, b = live ? bi % nb : 0;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (live) {
-      const float4 hv = *(const float4*)(h + ((size_t)t * NU + k) * F + 32 * b + 4 * sub);
-      v[0] = hv.x;
-      v[1] = hv.y;
-      v[2] = hv.z;
-      v[3] = hv.w;
-    }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = max8(amax);
-    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-    uint32_t pk = 0;
+  // h rows of the token's NU slots, quantized per 32 (8 lanes per block: the quantizer's arithmetic); the loads of
+  // four passes are issued before any is quantized (each is an L2 round trip)
+  constexpr int QB = 4;
+  for (int b00 = 0; b00 < NU * nb; b00 += 32 * QB) {
+    float4 hv[QB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pk |= (uint32_t)((int)__builtin_rintf(v[i] * inv) & 0xFF) << (8 * i);
-    if (live) {
-      *(uint32_t*)(sq + (size_t)k * F + (size_t)(sub >> 2) * nb * 16 + b * 16 + 4 * (sub & 3)) = pk;
-      if (sub == 0) ssc[k * nb + b] = amax / 127.0f;
+    for (int q = 0; q < QB; ++q) {
+      const int bi = b00 + 32 * q + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+      hv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (bi < NU * nb) hv[q] = *(const float4*)(h + ((size_t)t * NU + bi / nb) * F + 32 * (bi % nb) + 4 * sub);
+    }
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const int bi = b00 + 32 * q + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+      const bool live = bi < NU * nb;
+      const int k = live ? bi / nb : 0, b = live ? bi % nb : 0;
+      const float v[4] = {hv[q].x, hv[q].y, hv[q].z, hv[q].w};
+      float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      amax = max8(amax);
+      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+      uint32_t pk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk |= (uint32_t)((int)__builtin_rintf(v[i] * inv) & 0xFF) << (8 * i);
+      if (live) {
+        *(uint32_t*)(sq + (size_t)k * F + (size_t)(sub >> 2) * nb * 16 + b * 16 + 4 * (sub & 3)) = pk;
+        if (sub == 0) ssc[k * nb + b] = amax / 127.0f;
+      }
     }
   }
   __syncthreads();
