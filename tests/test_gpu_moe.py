@@ -166,3 +166,33 @@ def test_moe_decode_masked_logits(qm, dev, T):
     # (per token row: h's int8 requantization per 32 may round one value the other way where the GPU's f32 h and
     #  the oracle's differ in the last place, moving that row by up to ~1e-3)
     assert max(rows) < 2e-3, rows
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_decode_graph_replays(qm, dev, T):
+    """The decode-size path (routing inside the gate/up launch, then down) captured in a HIP graph: every replay, with
+    eager launches of the same call between replays, matches the eager result bit for bit."""
+    import torch
+    NE, E, Fd, NU = 64, 512, 256, 4
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=31 + T)
+    stream = torch.cuda.Stream()
+    out_g = torch.zeros_like(s["out"])
+    with torch.cuda.stream(stream):
+        qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], out_g, s["ws"])
+    stream.synchronize()
+    eager = out_g.clone()
+    ref = oracle.moe_forward(F.IQ4_XS, s["Wg"], F.IQ4_XS, s["Wu"], F.IQ4_XS, s["Wd"], NE, E, Fd, s["lg"], NU,
+                             s["aq"].cpu().numpy(), s["asc"].cpu().numpy())
+    assert rel_err(eager.cpu().numpy(), ref) < 1e-4
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], out_g, s["ws"])
+    for _ in range(4):
+        out_g.fill_(-1.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, eager)
+        other = torch.zeros_like(eager)
+        qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], other, s["ws"])
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager)
