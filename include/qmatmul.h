@@ -159,8 +159,9 @@ int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_st
  * go to qmatmul_prepare_weight straight from the mapping (raw_on_device = 0; rows = dims[1] * dims[2] * ..., K =
  * dims[0]). Replaces the reference's GgufFile (src/gguf.h:85-305; Win32 mapping there, POSIX here). A split model
  * (name-00001-of-0000N.gguf, "split.count" metadata) is opened from part 1: the other parts are mapped from the same
- * directory and their tensors appended (src/gguf.h:170-187); a missing part fails the open. Pointers returned by the accessors live until qmatmul_gguf_close. Reading is bounds-checked:
- * truncated or malformed files fail with QM_ERR_ARG and a message. Metadata: numbers of any GGUF numeric type read
+ * directory and their tensors appended (src/gguf.h:170-187); a missing part fails the open. Pointers returned by
+ * the accessors live until qmatmul_gguf_close. Reading is bounds-checked: truncated or malformed files fail with
+ * QM_ERR_ARG and a message. Metadata: numbers of any GGUF numeric type read
  * through get_int / get_float; strings through get_str; arrays are indexed but not exposed. */
 typedef struct qm_gguf qm_gguf;
 int qmatmul_gguf_open(const char* path, qm_gguf** out);
