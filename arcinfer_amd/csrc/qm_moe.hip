@@ -20,12 +20,20 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   if (counts)
     for (int e = threadIdx.x; e < NE; e += 256) hist[e] = 0;
   __syncthreads();
+  // the next token's logits are loaded while the current one is selected
+  const int t0 = (blockIdx.x * 4 + wave) * tpw;
+  float nv[PER_LANE];
+  if (t0 < T) route_load<PER_LANE>(logits + (size_t)t0 * ldl, NE, lane, nv);
   for (int j = 0; j < tpw; ++j) {
-    const int t = (blockIdx.x * 4 + wave) * tpw + j;
+    const int t = t0 + j;
     if (t >= T) break;
+    float v[PER_LANE];
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) v[i] = nv[i];
+    if (j + 1 < tpw && t + 1 < T) route_load<PER_LANE>(logits + (size_t)(t + 1) * ldl, NE, lane, nv);
     int my_e;
     float my_w;
-    route_token<PER_LANE>(logits + (size_t)t * ldl, NE, NU, lane, my_e, my_w);
+    route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w);
     if (lane < NU) {
       ids[(size_t)t * NU + lane] = my_e;
       wts[(size_t)t * NU + lane] = my_w;

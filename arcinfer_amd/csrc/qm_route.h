@@ -10,18 +10,22 @@
 
 namespace qm {
 
-// lg: the token's NE logits; lane < NU receives the k = lane-th selected expert and its weight
+// v[i] = logit i * 64 + lane of the token's NE logits lg (-inf past NE)
 template <int PER_LANE>
-__device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE, int NU, int lane, int& my_e,
-                                            float& my_w) {
-  float v[PER_LANE];
-  float mx = -INFINITY;
+__device__ __forceinline__ void route_load(const float* __restrict__ lg, int NE, int lane, float (&v)[PER_LANE]) {
 #pragma unroll
   for (int i = 0; i < PER_LANE; ++i) {
     const int e = i * 64 + lane;
     v[i] = e < NE ? lg[e] : -INFINITY;
-    mx = fmaxf(mx, v[i]);
   }
+}
+
+// the selection from the loaded logits (route_load); lane < NU receives the k = lane-th selected expert and its weight
+template <int PER_LANE>
+__device__ __forceinline__ void route_select(float (&v)[PER_LANE], int NE, int NU, int lane, int& my_e, float& my_w) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) mx = fmaxf(mx, v[i]);
   mx = wave_max(mx);
   float sum = 0.0f, my_p = 0.0f;
   unsigned taken = 0;  // bit i: expert i * 64 + lane selected
@@ -55,6 +59,15 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE
     }
   }
   my_w = my_p / sum;
+}
+
+// lg: the token's NE logits; lane < NU receives the k = lane-th selected expert and its weight
+template <int PER_LANE>
+__device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE, int NU, int lane, int& my_e,
+                                            float& my_w) {
+  float v[PER_LANE];
+  route_load<PER_LANE>(lg, NE, lane, v);
+  route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w);
 }
 
 }  // namespace qm
