@@ -83,7 +83,10 @@ def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
 
 @pytest.mark.parametrize("qtype", GEMV_TYPES)
 @pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (200, 2048, 1), (72, 17408, 1), (96, 5120, 2), (64, 1536, 5),
-                                   (64, 34816, 1), (24, 33024, 3)])  # (K > 32768: the generic kernel)
+                                   (64, 34816, 1), (24, 33024, 3),  # (K > 32768: the generic kernel)
+                                   # tokens per launch capped at 4 (6 blocks per lane; Q6_K beyond 4, the IQ2 grids
+                                   # beyond 3): 8 tokens as two launches, 6 as 4 + 2
+                                   (48, 6144, 8), (32, 5120, 8), (40, 4096, 6)])
 def test_gemv_f32_parity(qm, dev, qtype, N, K, T):
     import torch
     rng = np.random.default_rng(qtype * 3 + N)
