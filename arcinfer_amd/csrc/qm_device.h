@@ -319,6 +319,14 @@ __device__ __forceinline__ float wave_sum_width(float v, int width) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// max over the 32-lane half of the wave holding the lane; every lane receives it
+__device__ __forceinline__ float max32(float v) {
+  v = max8(v);
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  const float r0 = readlane_f(v, 0), r1 = readlane_f(v, 16), r2 = readlane_f(v, 32), r3 = readlane_f(v, 48);
+  return (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
+}
+
 // max over the wave; every lane receives it
 __device__ __forceinline__ float wave_max(float v) {
   v = max8(v);

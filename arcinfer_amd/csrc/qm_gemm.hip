@@ -471,9 +471,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         // (lanes of one half) are one 32-block of the h row, as moe_quant (zero/kernels/moe.cl:251-282)
         const float g = acc[mt][r];
         const float h = acc2[mt][r] * (g / (1.0f + expf(-g)));
-        float amax = fabsf(h);
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const float amax = max32(fabsf(h));
         const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
         const int q = (int)__builtin_rintf(h * inv);
         if (row_ok && col_ok) {
