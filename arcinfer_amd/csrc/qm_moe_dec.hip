@@ -20,14 +20,14 @@ __device__ __forceinline__ int block_isum(const RawBlk& r, const typename LdsFor
 
 }  // namespace
 
-// Gate/up: grid (slots, F / 8), routing included (logits non-null; else ids holds the routing). Wave 0 of every
-// work-group routes the slot's token (route_token:
+// Gate/up: grid (slots, F / (256 / LPR)), routing included (logits non-null; else ids holds the routing). Wave 0
+// of every work-group routes the slot's token (route_token:
 // the route kernel's arithmetic, so every work-group of a token selects the same experts) while the work-group stages
 // the token's int8 row in LDS (two 16-byte planes per 32-block, as the decode GEMV); the work-groups with
-// blockIdx.y == 0 of the token's first slot publish ids / wts for the down kernel. Then its 8 lane groups of 32 take
-// one expert row j each: g = gate_e[j] . a_t, u = up_e[j] . a_t, h[slot][j] = u * silu(g). CH = ceil(E / 1024) blocks
+// blockIdx.y == 0 of the token's first slot publish ids / wts for the down kernel. Then its lane groups of LPR take
+// one expert row j each: g = gate_e[j] . a_t, u = up_e[j] . a_t, h[slot][j] = u * silu(g). CH >= E / (32 LPR) blocks
 // per lane.
-template <int TYPE, int CH, int PER_LANE>
+template <int TYPE, int CH, int PER_LANE, int LPR = 32>
 __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView up, const float* __restrict__ logits,
                                                              int ldl, int NE, int* __restrict__ ids,
                                                              float* __restrict__ wts, int NU, int F,
@@ -64,13 +64,14 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
   for (int b = threadIdx.x; b < nb; b += 256) ssc[b] = asc[(size_t)b * M_stride + t];
   __syncthreads();
   const int e = sel[k];
-  const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
-  const int j = min((int)blockIdx.y * 8 + grp, F - 1);
+  constexpr int RPW = 256 / LPR;  // expert rows per work-group
+  const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
+  const int j = min((int)blockIdx.y * RPW + grp, F - 1);
   const size_t row = (size_t)e * F + j;
   RawBlk rg[CH], ru[CH];
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
-    const int b = min(gl + 32 * u, nb - 1);
+    const int b = min(gl + LPR * u, nb - 1);
     rg[u] = load_block_at<TYPE>(gate.qs + row * nb * Tr::QB, gate.hdr + row * (nb / 8) * Tr::HB, b);
     ru[u] = load_block_at<TYPE>(up.qs + row * nb * Tr::QB, up.hdr + row * (nb / 8) * Tr::HB, b);
   }
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
   float g = 0.0f, uu = 0.0f;
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
-    const int b = gl + 32 * u;
+    const int b = gl + LPR * u;
     if (b < nb) {
       float d;
       const int ig = block_isum<TYPE>(rg[u], &lds, b, kv, sq, nb, d);
@@ -87,9 +88,9 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
       uu += ssc[b] * d * (float)iu;
     }
   }
-  g = wave_sum_width(g, 32);
-  uu = wave_sum_width(uu, 32);
-  if (gl == 0 && (int)blockIdx.y * 8 + grp < F) h[(size_t)slot * F + j] = uu * (g / (1.0f + expf(-g)));
+  g = wave_sum_width(g, LPR);
+  uu = wave_sum_width(uu, LPR);
+  if (gl == 0 && (int)blockIdx.y * RPW + grp < F) h[(size_t)slot * F + j] = uu * (g / (1.0f + expf(-g)));
 }
 
 // Down + combine: grid (T, ceil(E / GPW)). The work-group quantizes its token's NU rows of h per 32 into LDS (two
@@ -177,18 +178,20 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
 }
 
 template <int TYPE, int PL>
-static void gateup_dec(const dim3& gg, size_t shg, int nbE, const WView& gate, const WView& up, const float* logits,
+static void gateup_dec(int slots, size_t shg, int nbE, const WView& gate, const WView& up, const float* logits,
                        int ldl, int NE, int* ids, float* wts, int NU, int F, const int8_t* aq, const float* asc,
                        int M_stride, float* h, hipStream_t s) {
-#define QM_GUD(CH) \
-  moe_gateup_dec_kernel<TYPE, CH, PL><<<gg, 256, shg, s>>>(gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h)
-  switch ((nbE + 31) / 32) {
-    case 1: QM_GUD(1); break;
-    case 2: QM_GUD(2); break;
-    case 3:
-    case 4: QM_GUD(4); break;
-    default: QM_GUD(8); break;
-  }
+  // 16 lanes per expert row up to 64 blocks per row (16 rows per work-group: half the work-groups, each routing and
+  // staging the token once; measured faster at 4 and 8 tokens, equal at 1), 32 lanes beyond
+#define QM_GUD(CH, LPR)                                                                                       \
+  moe_gateup_dec_kernel<TYPE, CH, PL, LPR><<<dim3((unsigned)slots, (unsigned)((F + 256 / LPR - 1) / (256 / LPR))), \
+                                              256, shg, s>>>(gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc,   \
+                                                             M_stride, h)
+  if (nbE <= 16) QM_GUD(1, 16);
+  else if (nbE <= 32) QM_GUD(2, 16);
+  else if (nbE <= 64) QM_GUD(4, 16);
+  else if (nbE <= 128) QM_GUD(4, 32);
+  else QM_GUD(8, 32);
 #undef QM_GUD
 }
 
@@ -198,7 +201,6 @@ static hipError_t moe_dec_typed(const WView& gate, const WView& up, const WView&
                                 const float* asc, int M_stride, float* h, float* x, int accumulate, hipStream_t s) {
   const int slots = T * NU, nbE = E / 32, nbF = F / 32;
   const size_t shg = (size_t)E + sizeof(float) * nbE;
-  const dim3 gg((unsigned)slots, (unsigned)((F + 7) / 8));
   if (T > 4) {
     // (more tokens: every gate/up work-group routing its token in front of its weight loads costs more than a
     //  separate route launch; measured at T = 8)
@@ -206,8 +208,8 @@ static hipError_t moe_dec_typed(const WView& gate, const WView& up, const WView&
     if (e != hipSuccess) return e;
     logits = nullptr;
   }
-  if (NE <= 256) gateup_dec<TYPE, 4>(gg, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
-  else gateup_dec<TYPE, 16>(gg, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
+  if (NE <= 256) gateup_dec<TYPE, 4>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
+  else gateup_dec<TYPE, 16>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, NU, F, aq, asc, M_stride, h, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t shd = (size_t)NU * F + sizeof(float) * NU * nbF;
