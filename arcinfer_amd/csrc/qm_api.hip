@@ -370,7 +370,9 @@ int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const i
   a.ldc = ldc;
   a.c_off = c_off;
   a.accumulate = accumulate;
-  const hipError_t e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
+  const hipError_t e = qm::f16_gemm_supported(w->type, M, w->view.K)
+                           ? qm::launch_gemm_f16(w->type, a, nullptr, (hipStream_t)stream)
+                           : qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm");
 }
 
@@ -386,7 +388,10 @@ int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_st
   a.M = M;
   a.M_stride = M_stride;
   a.dbg_isum = isum;
-  const hipError_t e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
+  // (the same kernel choice as qmatmul_gemm makes for this type and shape)
+  const hipError_t e = qm::f16_gemm_supported(w->type, M, w->view.K)
+                           ? qm::launch_gemm_f16(w->type, a, nullptr, (hipStream_t)stream)
+                           : qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm_blocksums");
 }
 

@@ -50,6 +50,11 @@ struct GemmArgs {
 };
 enum GemmMode : int { GEMM_DENSE = 0, GEMM_MOE_GATEUP = 1, GEMM_MOE_DOWN = 2 };
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
+// Prompt GEMM on the f16 matrix pipe (qm_gemm_f16.hip): the types and shapes it takes, its per-call workspace, and
+// the launcher (ws = null: the workspace comes from a per-device stream-ordered pool). dbg_isum: block-sum mode.
+bool f16_gemm_supported(int type, int M, int K);
+size_t f16_workspace_bytes(int M, int K);
+hipError_t launch_gemm_f16(int type, const GemmArgs& a, void* ws, hipStream_t s);
 // slots per MoE tile (one expert each); a 64-row tile (fewer, larger tiles) measured slower under the Zipf skew
 constexpr int kMoeTileRows = 32;
 
