@@ -376,6 +376,44 @@ int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const i
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm");
 }
 
+int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
+                         int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream) {
+  if (int st = check_acts("qmatmul_gemm_noalloc", w, aq, asc, absum, M, M_stride)) return st;
+  if (!C) return fail(QM_ERR_ARG, "qmatmul_gemm_noalloc: null output");
+  if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm_noalloc: rows %d not a multiple of 16", w->rows);
+  if (accumulate < 0 || accumulate > 2)
+    return fail(QM_ERR_ARG, "qmatmul_gemm_noalloc: accumulate %d (0..2)", accumulate);
+  if (c_off < 0 || ldc < c_off + w->rows)
+    return fail(QM_ERR_SHAPE, "qmatmul_gemm_noalloc: ldc %d, c_off %d, rows %d", ldc, c_off, w->rows);
+  QM_CHECK_INIT();
+  qm::GemmArgs a{};
+  a.w = w->view;
+  a.aq = aq;
+  a.asc = asc;
+  a.absum = absum;
+  a.M = M;
+  a.M_stride = M_stride;
+  a.C = C;
+  a.ldc = ldc;
+  a.c_off = c_off;
+  a.accumulate = accumulate;
+  hipError_t e;
+  if (qm::f16_gemm_supported(w->type, M, w->view.K)) {
+    void* scr = nullptr;
+    size_t cap = 0;
+    e = qm::f16_scratch(&scr, &cap);
+    if (e != hipSuccess) return hip_fail(e, "qmatmul_gemm_noalloc: scratch lookup");
+    const size_t need = qm::f16_workspace_bytes(M, w->view.K);
+    if (need > cap)
+      return fail(QM_ERR_WORKSPACE, "qmatmul_gemm_noalloc: M %d x K %d needs %zu bytes of scratch, the static scratch "
+                  "holds %zu (use qmatmul_gemm)", M, w->view.K, need, cap);
+    e = qm::launch_gemm_f16(w->type, a, scr, (hipStream_t)stream);
+  } else {
+    e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);  // (this kernel uses no scratch)
+  }
+  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm_noalloc");
+}
+
 int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream) {
   static const float unused = 0.0f;  // (the block-sum mode reads no scales or sums)
   if (int st = check_acts("qmatmul_gemm_blocksums", w, aq, &unused, (const int16_t*)&unused, M, M_stride)) return st;

@@ -20,6 +20,8 @@
 // 32x32 result layout: lane l holds column l % 32 and rows 8 * (r / 4) + 4 * (l / 32) + r % 4, r = 0..15.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "qm_decode.h"
 #include "qm_launch.h"
 
@@ -374,6 +376,32 @@ static hipError_t f16_pool(hipMemPool_t* out) {
     pools[dev] = p;
   }
   *out = pools[dev];
+  return hipSuccess;
+}
+
+// Allocation-free workspace for qmatmul_gemm_noalloc: a file-scope device array (each GPU holds its own copy until
+// the process ends). Host code never passes the array's name to a kernel or a copy -- in host code it is only a
+// stand-in for the symbol -- but the device address that hipGetSymbolAddress returns for the current device, looked
+// up once per device (under a lock) and kept.
+constexpr size_t kF16ScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kF16ScratchBytes];
+
+hipError_t f16_scratch(void** out, size_t* bytes) {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  *bytes = kF16ScratchBytes;
   return hipSuccess;
 }
 

@@ -55,6 +55,8 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
 bool f16_gemm_supported(int type, int M, int K);
 size_t f16_workspace_bytes(int M, int K);
 hipError_t launch_gemm_f16(int type, const GemmArgs& a, void* ws, hipStream_t s);
+// The current device's copy of the static scratch array (device address and size) for the allocation-free entry
+hipError_t f16_scratch(void** ptr, size_t* bytes);
 // slots per MoE tile (one expert each); a 64-row tile (fewer, larger tiles) measured slower under the Zipf skew
 constexpr int kMoeTileRows = 32;
 

@@ -29,6 +29,7 @@ SIGNATURES = [
     ("qmatmul_quantize_act", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_gemv", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_gemm", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    ("qmatmul_gemm_noalloc", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_moe_workspace_size", _Z, [_I, _I, _I, _I, _I]),
     ("qmatmul_moe_route", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_moe_grouped", _I, [_P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _Z, _P]),
@@ -167,14 +168,15 @@ def gemv(w, aq, asc, absum, T=1, C=None, ldc=None, c_off=0, accumulate=0, stream
     return C
 
 
-def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None):
+def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None, noalloc=False):
+    """qmatmul_gemm (noalloc=True: qmatmul_gemm_noalloc, the entry point that allocates no device memory)."""
     import torch
     Ms = aq.shape[0]
     M = Ms if M is None else M
     if C is None:
         C = torch.empty((M, w.rows), dtype=torch.float32, device=aq.device)
         ldc = w.rows
-    _call("qmatmul_gemm", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, _ptr(C),
+    _call("qmatmul_gemm_noalloc" if noalloc else "qmatmul_gemm", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, _ptr(C),
           w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
     return C
 

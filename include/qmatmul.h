@@ -110,12 +110,24 @@ int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, floa
 int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,
                  float* C, int ldc, int c_off, int accumulate, void* stream);
 
-/* Prompt GEMM on int8 MFMA: C[m*ldc + c_off + n] (op)= sum_k W[n][k] * a_m[k] for m < M.
+/* Prompt GEMM: C[m*ldc + c_off + n] (op)= sum_k W[n][k] * a_m[k] for m < M.
  * M <= M_stride; any M >= 1 and rows(w) % 16 == 0. Replaces decode_w8 + gemm of Engine::matmul1 for T > 8 and
  * gemm_ext (zero/engine.h:3234-3297; zero/kernels/gemm.cl:132-475). Q4_K is computed exactly (scales and mins),
- * not requantized as the reference's W8 path does (zero/kernels/decode.cl:455-507). */
+ * not requantized as the reference's W8 path does (zero/kernels/decode.cl:455-507). Q4_K with M >= 128 runs on the
+ * f16 matrix pipe (exact integer block sums from f16 products) and takes a per-call workspace of about 2*M*K bytes
+ * from a per-device stream-ordered memory pool; every other case runs on int8 MFMA and allocates nothing. */
 int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                  float* C, int ldc, int c_off, int accumulate, void* stream);
+
+/* qmatmul_gemm without any device allocation. No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same arguments, results and kernels
+ * as qmatmul_gemm; where qmatmul_gemm would take its pool workspace, this entry uses a static 32 MiB device array
+ * (one per GPU, held until the process ends) and returns QM_ERR_WORKSPACE when the call needs more
+ * (f16 path: 2*Mp*K + 4*Mp*K/32 bytes, Mp = M rounded up to 128; e.g. M 2048 x K 5120 needs 22.3 MB).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different streams, or threads) race
+ * and must be ordered by the caller. Each call writes every scratch byte it reads before reading it. */
+int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
+                         int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream);
 
 /* Workspace bytes of qmatmul_moe_grouped for T tokens, NE experts, NU experts per token, hidden E, expert width F. */
 size_t qmatmul_moe_workspace_size(int T, int NE, int NU, int E, int F);
