@@ -517,8 +517,7 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   float* hsc = (float*)(b + L.hsc);
   float* y = (float*)(b + L.y);
   // decode sizes: GEMV-shaped expert kernels (no tiles, no scatter): routing inside the gate/up launch, then down
-  static const int dec_env = getenv("QM_MOE_DECODE") ? atoi(getenv("QM_MOE_DECODE")) : 1;
-  if (dec_env && T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192 && down->type == gate->type) {
+  if (T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192 && down->type == gate->type) {
     const hipError_t e = qm::launch_moe_decode(gate->type, gate->view, up->view, down->view, T, NU, E, F, logits, ldl,
                                                NE, ids, wts, aq, asc, M_stride, (float*)(b + L.hf), x, accumulate, s);
     return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");

@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
           pay2[b] = load_payload<TYPE>(a.w2, n, sn * 8 + b, hf);
         }
       }
-      if constexpr (MODE == GEMM_DENSE && !DUMP && MT == 2) {
+      if constexpr (MODE == GEMM_DENSE && MT == 2) {
         // both row tiles' MFMAs first, then the epilogues: row tile 0's VALU epilogue runs while row tile 1's
         // MFMAs execute, and row tile 1's epilogue while row tile 0's mins MFMA does
         v16i dv[2][2];
@@ -361,9 +361,23 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
             dv[mt][q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[q], zero16, 0, 0, 0);
           }
-          const float my_asc = L.asc[cur][(2 * p + hf) * BM + mt * 32 + lc];
-          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
+          if constexpr (!DUMP) {
+            const float my_asc = L.asc[cur][(2 * p + hf) * BM + mt * 32 + lc];
+            sc[mt] = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc, zero32, 0, 0, 0);
+          }
         }
+        if constexpr (DUMP) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3), blk = s * 8 + 2 * p + q;
+                if (i < nvalid && n_loc < n_rows)
+                  a.dbg_isum[((size_t)(m0 + i) * n_rows + n_loc) * nb + blk] = isc[2 * p + q] * dv[mt][q][r];
+              }
+        } else {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -378,6 +392,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
           }
+        }
         }
       } else
 #pragma unroll
@@ -687,14 +702,11 @@ static hipError_t go(const GemmArgs& a, hipStream_t s) {
 
 template <int TYPE>
 static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
-  if (a.dbg_isum) return go<TYPE, 1, GEMM_DENSE, true>(a, s);
+  // (the block-sum mode takes the product's row-tile count, so the sums checked are those of the kernel that runs)
+  if (a.dbg_isum) return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, true>(a, s) : go<TYPE, 2, GEMM_DENSE, true>(a, s);
   switch (mode) {
-    case GEMM_DENSE: {
-      // QM_GEMM_MT=1|2 overrides the row tiles per work-group (32 or 64 activation rows)
-      static const int mt_env = getenv("QM_GEMM_MT") ? atoi(getenv("QM_GEMM_MT")) : 0;
-      const int mt = mt_env == 1 || mt_env == 2 ? mt_env : (a.M <= 32 ? 1 : 2);
-      return mt == 1 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
-    }
+    case GEMM_DENSE:
+      return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
     case GEMM_MOE_GATEUP: return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN: return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
     default: return hipErrorInvalidValue;
@@ -704,7 +716,7 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
 template <int TYPE>
 static hipError_t dispatch_s16(int mode, const GemmArgs& a, hipStream_t s) {
   if (mode != GEMM_DENSE) return hipErrorInvalidValue;
-  if (a.dbg_isum) return go_s16<TYPE, 1, true>(a, s);
+  if (a.dbg_isum) return a.M <= 32 ? go_s16<TYPE, 1, true>(a, s) : go_s16<TYPE, 2, true>(a, s);
   return a.M <= 32 ? go_s16<TYPE, 1, false>(a, s) : go_s16<TYPE, 2, false>(a, s);
 }
 

@@ -106,90 +106,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Batch-1 decode GEMV (the token-generation case). The token's int8 row, its per-32 scales (and, for Q4_K, per-32
-// sums) are staged in LDS once per work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each
-// 32-block) so 32 lanes reading consecutive blocks read consecutive 16-byte words. A 32-lane group owns one row at a
-// time: lane j takes blocks j, j + 32, ... of the row, CH of them per step, and the next step's weight loads (next
-// chunk or next row) are issued before the current step is decoded, so every lane keeps 2*CH 16-byte streaming loads
-// in flight. Each group walks `rpg` rows spaced 8 apart (the work-group's 8 groups interleave rows). Requires K/32 to
-// be a multiple of 32.
-template <int TYPE, int CH, bool EXACT>
-__global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a, int rpg) {
-  extern __shared__ uint4 smem[];
-  const int K = a.w.K, nb = K / 32, rows = a.w.rows;
-  uint8_t* sq = (uint8_t*)smem;            // [2][nb][16] int8 planes
-  float* ssc = (float*)(sq + (size_t)K);    // [nb] scales
-  int* sbs = (int*)(ssc + nb);              // [nb] per-16 sums of each block, packed int16 pairs (Q4_K, Q6_K)
-  const int grp = threadIdx.x >> 5, gl = threadIdx.x & 31;
-  const int nch = (nb / 32 + CH - 1) / CH;  // steps per row
-  const int row_base = blockIdx.x * 8 * rpg + grp;
-  const int steps = rpg * nch;
-
-  RawBlk cur[CH], nxt[CH];
-  using Tr = Traits<TYPE>;
-  auto fetch = [&](int step, RawBlk* dst) {
-    const int i = step / nch, c = step % nch;
-    const int n = min(row_base + 8 * i, rows - 1);
-    const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
-    const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + 32 * (c * CH + u);
-      dst[u] = load_block_at<TYPE>(qrow, hrow, EXACT ? b : min(b, nb - 1));
-    }
-  };
-  fetch(0, cur);
-  // (the first weight loads are in flight while the activations are staged)
-  __shared__ typename LdsFor<TYPE>::type lds;
-  lds_fill<TYPE>(&lds);
-  for (int i = threadIdx.x; i < 2 * nb; i += 256) {
-    const int b = i >> 1, h = i & 1;
-    *(uint4*)(sq + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + 32 * b + 16 * h);
-  }
-  for (int b = threadIdx.x; b < nb; b += 256) {
-    ssc[b] = a.asc[(size_t)b * a.M_stride];
-    if constexpr (kNeedsBsum<TYPE>)
-      sbs[b] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride] | ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride] << 16);
-  }
-  __syncthreads();
-
-  const KvTab kv = kv_tab();
-  float acc = 0.0f;
-  for (int step = 0; step < steps; ++step) {
-    if (step + 1 < steps) fetch(step + 1, nxt);
-    const int i = step / nch, c = step % nch;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int b = gl + 32 * (c * CH + u);
-      if (EXACT || b < nb) {
-        const uint4 x0 = *(const uint4*)(sq + b * 16), x1 = *(const uint4*)(sq + (size_t)nb * 16 + b * 16);
-        const int bp = kNeedsBsum<TYPE> ? sbs[b] : 0;
-        const BlockInts bi = block_product<TYPE>(cur[u], &lds, b & 7, kv, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16);
-        acc += block_value<TYPE>(ssc[b], bi);
-      }
-    }
-    if (c == nch - 1) {
-      const float v = wave_sum_width(acc, 32);
-      const int n = row_base + 8 * i;
-      if (gl == 0 && n < rows) {
-        float* cp = a.C + a.c_off + n;
-        *cp = a.accumulate ? *cp + v : v;
-      }
-      acc = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < CH; ++u) cur[u] = nxt[u];
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
 // Batch-1 decode GEMV, persistent sweep. LPR lanes share a row (32, or 128 = two waves with an LDS combine); lane j
 // takes blocks j, j + LPR, ... (CH of them). The grid is a few work-groups per CU and lane group g walks rows
 // g, g + G, g + 2G, ... (G = lane groups in the grid), so the whole grid moves through the weight matrix together
 // and every group has one row in flight: it decodes the row once its loads land and only then issues the next row's
-// loads. Measured on MI355X this beats both issuing every row's loads up front (the decode then piles up behind the
-// stream) and keeping two rows in flight per group. The token's activations are staged in LDS once per work-group, as in gemv1_kernel.
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF>
+// loads. Measured on MI355X this beats issuing every row's loads up front (the decode then piles up behind the
+// stream). The token's int8 row, its per-32 scales (and Q4_K / Q5_K / Q6_K per-16 sums) are staged in LDS once per
+// work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
+// consecutive blocks read consecutive 16-byte words. DUMP: the same kernel writes each block's int32 sums
+// (dbg_isum, and Q4_K / Q5_K min sums to dbg_msum) instead of the output.
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP>
 __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   extern __shared__ uint4 smem[];
   using Tr = Traits<TYPE>;
@@ -228,7 +154,7 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   }
   for (int i = threadIdx.x; i < nb * TB; i += 256) {
     const int t = i / nb, b = i % nb, tt = min(t, T - 1);
-    ssc[i] = a.asc[(size_t)b * a.M_stride + tt];
+    if constexpr (!DUMP) ssc[i] = a.asc[(size_t)b * a.M_stride + tt];  // (the block-sum mode has no scales)
     if constexpr (kNeedsBsum<TYPE>)
       sbs[i] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride + tt] |
                ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt] << 16);
@@ -254,7 +180,16 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
           const uint4 x0 = *(const uint4*)(st + b * 16), x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
           const int bp = kNeedsBsum<TYPE> ? sbs[t * nb + b] : 0;
           block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16, bi.iv, bi.mv);
-          acc[t] += block_value<TYPE>(ssc[t * nb + b], bi);
+          if constexpr (DUMP) {
+            const int n = g0 + G * i;
+            if (n < rows && t < T) {
+              const size_t o = ((size_t)t * rows + n) * nb + b;
+              a.dbg_isum[o] = bi.iv;
+              if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = bi.mv;
+            }
+          } else {
+            acc[t] += block_value<TYPE>(ssc[t * nb + b], bi);
+          }
         }
       }
     }
@@ -277,7 +212,7 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
         for (int k = 1; k < WPR; ++k) v[t] += part[i & 1][grp][k][t];
       }
     }
-    if (gl == 0 && n < rows) {
+    if (!DUMP && gl == 0 && n < rows) {
 #pragma unroll
       for (int t = 0; t < TB; ++t)
         if (t < T) {
@@ -317,7 +252,7 @@ static size_t gemvs_lds(int type, int K, int TB) {
   return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
 }
 
-template <int TYPE, int LPR, int CH, bool EXACT, int TB>
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP>
 static hipError_t gos(const GemvArgs& a, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
   constexpr int PF = TB == 1 ? 2 : 1;  // batch 1: two rows in flight per lane group; more tokens: registers to tokens
@@ -327,7 +262,7 @@ static hipError_t gos(const GemvArgs& a, hipStream_t s) {
   static const int per_cu = [] {
     int n = 0;
     const size_t lds_max = gemvs_lds(TYPE, 32 * LPR * CH, TB);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF>, 256, lds_max) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false>, 256, lds_max) !=
             hipSuccess || n < 1)
       n = 1;
     return min(2, n);
@@ -340,33 +275,20 @@ static hipError_t gos(const GemvArgs& a, hipStream_t s) {
     return n;
   }();
   const int wgs = min(per_cu * cus, (a.w.rows + GPW - 1) / GPW);
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
 
-template <int TYPE, int LPR, int CH, bool EXACT>
+template <int TYPE, int LPR, int CH, bool EXACT, bool DUMP>
 static hipError_t gos_tb(const GemvArgs& a, hipStream_t s) {
   switch (a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8) {
-    case 1: return gos<TYPE, LPR, CH, EXACT, 1>(a, s);
-    case 2: return gos<TYPE, LPR, CH, EXACT, 2>(a, s);
-    case 4: return gos<TYPE, LPR, CH, EXACT, 4>(a, s);
+    case 1: return gos<TYPE, LPR, CH, EXACT, 1, DUMP>(a, s);
+    case 2: return gos<TYPE, LPR, CH, EXACT, 2, DUMP>(a, s);
+    case 4: return gos<TYPE, LPR, CH, EXACT, 4, DUMP>(a, s);
     default:
-      if constexpr (gemvs_max_tb<TYPE>(CH) >= 8) return gos<TYPE, LPR, CH, EXACT, 8>(a, s);
+      if constexpr (gemvs_max_tb<TYPE>(CH) >= 8) return gos<TYPE, LPR, CH, EXACT, 8, DUMP>(a, s);
       else return hipErrorInvalidValue;  // (the dispatcher never asks: it chunks by gemvs_max_tb)
   }
-}
-
-template <int TYPE, int CH, bool EXACT>
-static hipError_t go1(const GemvArgs& a, hipStream_t s) {
-  const int nb = a.w.K / 32;
-  // rows per 32-lane group: enough work-groups to fill 256 CUs twice, each group walking several rows
-  const int rows = a.w.rows;
-  int rpg = 1;
-  while (rpg < 16 && (rows + 8 * rpg * 2 - 1) / (8 * rpg * 2) >= 1024) rpg *= 2;
-  const unsigned grid = (unsigned)((rows + 8 * rpg - 1) / (8 * rpg));
-  const size_t shm = (size_t)a.w.K + sizeof(float) * nb + (kNeedsBsum<TYPE> ? sizeof(int) * nb : 0);
-  gemv1_kernel<TYPE, CH, EXACT><<<grid, 256, shm, s>>>(a, rpg);
-  return hipGetLastError();
 }
 
 template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S || kIq2<TYPE> ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
@@ -377,74 +299,70 @@ static hipError_t go(const GemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int TYPE>
-hipError_t gemv_dispatch(const GemvArgs& a, hipStream_t s) {
+// The route of one call: the sweep kernel for rows of up to 1024 blocks (K <= 32768), in token chunks; the generic
+// kernel beyond. The block-sum mode (DUMP) takes exactly the route, instantiation and token chunking of the
+// product, so the sums checked are those of the kernels that run.
+template <int TYPE, bool DUMP>
+static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
   const int nb = a.w.K / 32;
-  if (a.dbg_isum) {
-    switch (a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : 8) {
-      case 1: return go<TYPE, 8, 1, 1, true>(a, s);
-      case 2: return go<TYPE, 8, 1, 2, true>(a, s);
-      case 4: return go<TYPE, 8, 1, 4, true>(a, s);
-      default: return go<TYPE, 8, 1, 8, true>(a, s);
-    }
-  }
   const bool l32 = nb % 32 == 0;
-  static const int sweep = getenv("QM_GEMV_SWEEP") ? atoi(getenv("QM_GEMV_SWEEP")) : 1;
-  if (sweep && nb <= 1024) {
+  if (nb <= 1024) {
     // tokens per launch: as many as fit in 80 KB of LDS (two work-groups per CU), up to 8; more tokens -> chunks
     // of tokens, each launch reading the weights once
     int tb = gemvs_max_tb<TYPE>(nb <= 256 ? (nb + 31) / 32 : (nb + 127) / 128);
     const size_t cap = 80 * 1024 - sizeof(typename LdsFor<TYPE>::type);  // (the codebook tables' static LDS)
     while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > cap) tb >>= 1;
-    if (gemvs_lds(TYPE, a.w.K, tb) <= cap) {
-      for (int t0 = 0; t0 < a.T; t0 += tb) {
-        GemvArgs c = a;
-        c.T = min(tb, a.T - t0);
-        c.aq = a.aq + (size_t)t0 * a.w.K;
+    for (int t0 = 0; t0 < a.T; t0 += tb) {
+      GemvArgs c = a;
+      c.T = min(tb, a.T - t0);
+      c.aq = a.aq + (size_t)t0 * a.w.K;
+      if (!DUMP) {
         c.asc = a.asc + t0;
-        c.absum = a.absum + t0;
+        if (a.absum) c.absum = a.absum + t0;
         c.C = a.C + (size_t)t0 * a.ldc;
-        hipError_t e;
-        if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
-          switch ((nb + 31) / 32) {
-            case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true>(c, s) : gos_tb<TYPE, 32, 1, false>(c, s); break;
-            case 2: e = nb == 64 ? gos_tb<TYPE, 32, 2, true>(c, s) : gos_tb<TYPE, 32, 2, false>(c, s); break;
-            case 3: e = nb == 96 ? gos_tb<TYPE, 32, 3, true>(c, s) : gos_tb<TYPE, 32, 3, false>(c, s); break;
-            case 4: e = nb == 128 ? gos_tb<TYPE, 32, 4, true>(c, s) : gos_tb<TYPE, 32, 4, false>(c, s); break;
-            case 5: e = nb == 160 ? gos_tb<TYPE, 32, 5, true>(c, s) : gos_tb<TYPE, 32, 5, false>(c, s); break;
-            case 6: e = nb == 192 ? gos_tb<TYPE, 32, 6, true>(c, s) : gos_tb<TYPE, 32, 6, false>(c, s); break;
-            case 7: e = nb == 224 ? gos_tb<TYPE, 32, 7, true>(c, s) : gos_tb<TYPE, 32, 7, false>(c, s); break;
-            default: e = nb == 256 ? gos_tb<TYPE, 32, 8, true>(c, s) : gos_tb<TYPE, 32, 8, false>(c, s); break;
-          }
-        } else {  // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
-          switch ((nb + 127) / 128) {
-            case 3: e = nb == 384 ? gos_tb<TYPE, 128, 3, true>(c, s) : gos_tb<TYPE, 128, 3, false>(c, s); break;
-            case 4: e = nb == 512 ? gos_tb<TYPE, 128, 4, true>(c, s) : gos_tb<TYPE, 128, 4, false>(c, s); break;
-            case 5: e = nb == 640 ? gos_tb<TYPE, 128, 5, true>(c, s) : gos_tb<TYPE, 128, 5, false>(c, s); break;
-            case 6: e = nb == 768 ? gos_tb<TYPE, 128, 6, true>(c, s) : gos_tb<TYPE, 128, 6, false>(c, s); break;
-            case 7: e = nb == 896 ? gos_tb<TYPE, 128, 7, true>(c, s) : gos_tb<TYPE, 128, 7, false>(c, s); break;
-            default: e = nb == 1024 ? gos_tb<TYPE, 128, 8, true>(c, s) : gos_tb<TYPE, 128, 8, false>(c, s); break;
-          }
-        }
-        if (e != hipSuccess) return e;
+      } else {
+        if (a.absum) c.absum = a.absum + t0;
+        c.dbg_isum = a.dbg_isum + (size_t)t0 * a.w.rows * nb;
+        if (a.dbg_msum) c.dbg_msum = a.dbg_msum + (size_t)t0 * a.w.rows * nb;
       }
-      return hipSuccess;
+      hipError_t e;
+      if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
+        switch ((nb + 31) / 32) {
+          case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true, DUMP>(c, s) : gos_tb<TYPE, 32, 1, false, DUMP>(c, s); break;
+          case 2: e = nb == 64 ? gos_tb<TYPE, 32, 2, true, DUMP>(c, s) : gos_tb<TYPE, 32, 2, false, DUMP>(c, s); break;
+          case 3: e = nb == 96 ? gos_tb<TYPE, 32, 3, true, DUMP>(c, s) : gos_tb<TYPE, 32, 3, false, DUMP>(c, s); break;
+          case 4: e = nb == 128 ? gos_tb<TYPE, 32, 4, true, DUMP>(c, s) : gos_tb<TYPE, 32, 4, false, DUMP>(c, s); break;
+          case 5: e = nb == 160 ? gos_tb<TYPE, 32, 5, true, DUMP>(c, s) : gos_tb<TYPE, 32, 5, false, DUMP>(c, s); break;
+          case 6: e = nb == 192 ? gos_tb<TYPE, 32, 6, true, DUMP>(c, s) : gos_tb<TYPE, 32, 6, false, DUMP>(c, s); break;
+          case 7: e = nb == 224 ? gos_tb<TYPE, 32, 7, true, DUMP>(c, s) : gos_tb<TYPE, 32, 7, false, DUMP>(c, s); break;
+          default: e = nb == 256 ? gos_tb<TYPE, 32, 8, true, DUMP>(c, s) : gos_tb<TYPE, 32, 8, false, DUMP>(c, s); break;
+        }
+      } else {  // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
+        switch ((nb + 127) / 128) {
+          case 3: e = nb == 384 ? gos_tb<TYPE, 128, 3, true, DUMP>(c, s) : gos_tb<TYPE, 128, 3, false, DUMP>(c, s); break;
+          case 4: e = nb == 512 ? gos_tb<TYPE, 128, 4, true, DUMP>(c, s) : gos_tb<TYPE, 128, 4, false, DUMP>(c, s); break;
+          case 5: e = nb == 640 ? gos_tb<TYPE, 128, 5, true, DUMP>(c, s) : gos_tb<TYPE, 128, 5, false, DUMP>(c, s); break;
+          case 6: e = nb == 768 ? gos_tb<TYPE, 128, 6, true, DUMP>(c, s) : gos_tb<TYPE, 128, 6, false, DUMP>(c, s); break;
+          case 7: e = nb == 896 ? gos_tb<TYPE, 128, 7, true, DUMP>(c, s) : gos_tb<TYPE, 128, 7, false, DUMP>(c, s); break;
+          default: e = nb == 1024 ? gos_tb<TYPE, 128, 8, true, DUMP>(c, s) : gos_tb<TYPE, 128, 8, false, DUMP>(c, s); break;
+        }
+      }
+      if (e != hipSuccess) return e;
     }
-  }
-  if (a.T <= 1 && l32 && a.w.K <= 32768) {
-    const int per_lane = nb / 32;  // blocks per lane per row
-    if (per_lane % 5 == 0) return go1<TYPE, 5, true>(a, s);
-    if (per_lane % 4 == 0) return go1<TYPE, 4, true>(a, s);
-    return go1<TYPE, 6, false>(a, s);
+    return hipSuccess;
   }
   if (a.T <= 1) {
-    // short rows (many rows): 2 rows per lane group; long rows (few rows, K >= 8192): 1, for more waves in flight
-    if (l32) return a.w.K >= 8192 ? go<TYPE, 32, 1, 1, false>(a, s) : go<TYPE, 32, 2, 1, false>(a, s);
-    return go<TYPE, 8, 2, 1, false>(a, s);
+    // long rows (K > 32768: few rows): one row per lane group, for more waves in flight
+    return l32 ? go<TYPE, 32, 1, 1, DUMP>(a, s) : go<TYPE, 8, 2, 1, DUMP>(a, s);
   }
-  if (a.T <= 2) return l32 ? go<TYPE, 32, 1, 2, false>(a, s) : go<TYPE, 8, 1, 2, false>(a, s);
-  if (a.T <= 4) return l32 ? go<TYPE, 32, 1, 4, false>(a, s) : go<TYPE, 8, 1, 4, false>(a, s);
-  return l32 ? go<TYPE, 32, 1, 8, false>(a, s) : go<TYPE, 8, 1, 8, false>(a, s);
+  if (a.T <= 2) return l32 ? go<TYPE, 32, 1, 2, DUMP>(a, s) : go<TYPE, 8, 1, 2, DUMP>(a, s);
+  if (a.T <= 4) return l32 ? go<TYPE, 32, 1, 4, DUMP>(a, s) : go<TYPE, 8, 1, 4, DUMP>(a, s);
+  return l32 ? go<TYPE, 32, 1, 8, DUMP>(a, s) : go<TYPE, 8, 1, 8, DUMP>(a, s);
+}
+
+template <int TYPE>
+hipError_t gemv_dispatch(const GemvArgs& a, hipStream_t s) {
+  return a.dbg_isum ? gemv_route<TYPE, true>(a, s) : gemv_route<TYPE, false>(a, s);
 }
 
 }  // namespace qm
