@@ -471,22 +471,21 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = hipSuccess;
   if (counts) e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
-  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
+  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, nullptr, s);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_route");
 }
 
-int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
-                        int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,
-                        int accumulate, void* ws, size_t ws_bytes, void* stream) {
+int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE,
+                           const float* logits, int ldl, int T, int NU, const int8_t* aq, const float* asc,
+                           int M_stride, const float* escale, const float* sh, int ldsh, int sh_gated, float* x,
+                           int accumulate, void* ws, size_t ws_bytes, void* stream) {
   if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
   for (const qm_weight* w : {gate, up, down})
-    if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K || w->type == QM_IQ2_XS || w->type == QM_IQ2_S)
+    if (w->type == QM_Q4_K || w->type == QM_Q5_K)
       return fail(QM_ERR_TYPE,
-                  "qmatmul_moe_grouped: Q4_K, Q5_K, Q6_K, IQ2_XS and IQ2_S expert weights (per-16 sums or scales) are "
-                  "not supported");
-  if (gate->type != up->type)
-    return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: gate and up must have one type (got %d, %d)", gate->type, up->type);
+                  "qmatmul_moe_grouped: Q4_K and Q5_K expert weights (per-block mins) are not supported, as in the "
+                  "reference's expert GEMMs (zero/engine_moe.h:284-301)");
   if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)
     return fail(QM_ERR_SHAPE, "qmatmul_moe_grouped: NE %d, NU %d, T %d, M_stride %d, ldl %d", NE, NU, T, M_stride, ldl);
   const int E = gate->K, F = down->K;
@@ -496,6 +495,10 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
                 gate->rows, gate->K, up->rows, up->K, down->rows, down->K, NE);
   if (accumulate != 0 && accumulate != 1)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: accumulate %d (0 or 1)", accumulate);
+  if (sh && (ldsh < E || ldsh % 4 || !aligned(sh, 16)))
+    return fail(QM_ERR_ARG, "qmatmul_moe_grouped: sh needs ldsh >= E (%d), a multiple of 4, 16-byte alignment", E);
+  if (sh && sh_gated && ldl < NE + 1)
+    return fail(QM_ERR_SHAPE, "qmatmul_moe_grouped: a gated shared expert reads logits[t][NE]: ldl %d <= NE %d", ldl, NE);
   if (!aligned(aq, 16) || !aligned(x, 16) || !aligned(ws, 256))
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: aq/x need 16-byte, ws 256-byte alignment");
   const MoeLayout L = moe_layout(T, NE, NU, E, F);
@@ -516,16 +519,23 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
   int8_t* hq = (int8_t*)(b + L.hq);
   float* hsc = (float*)(b + L.hsc);
   float* y = (float*)(b + L.y);
-  // decode sizes: GEMV-shaped expert kernels (no tiles, no scatter): routing inside the gate/up launch, then down
-  if (T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192 && down->type == gate->type) {
-    const hipError_t e = qm::launch_moe_decode(gate->type, gate->view, up->view, down->view, T, NU, E, F, logits, ldl,
-                                               NE, ids, wts, aq, asc, M_stride, (float*)(b + L.hf), x, accumulate, s);
+  float* hf = (float*)(b + L.hf);
+  const qm::MoeShared shd{sh, ldsh, sh && sh_gated ? logits + NE : nullptr, ldl};
+  // decode sizes: GEMV-shaped expert kernels (no tiles, no scatter): routing with gate/up, then down + combine
+  if (T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192) {
+    const hipError_t e = qm::launch_moe_decode(gate->type, up->type, down->type, gate->view, up->view, down->view, T,
+                                               NU, E, F, logits, ldl, NE, escale, ids, wts, aq, asc, M_stride, hf, x,
+                                               accumulate, shd, s);
     return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
   }
   hipError_t e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
-  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, s);
+  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, escale, s);
   if (e == hipSuccess) e = qm::launch_moe_scan(counts, cursor, tstart, tiles, NE, L.tile_rows, s);
   if (e == hipSuccess) e = qm::launch_moe_scatter(ids, wts, L.slots, NU, NE, cursor, stok, swt, inv, s);
+  // gate and up: one launch when they share a type the int8 kernel takes in one pass; otherwise the gate projection
+  // into hf, then the up projection forming h from it
+  const bool s16 = [](int t) { return t == QM_Q6_K || t == QM_IQ2_XS || t == QM_IQ2_S; }(gate->type);
+  const bool fused = gate->type == up->type && !s16;
   if (e == hipSuccess) {
     qm::GemmArgs a{};
     a.w = gate->view;
@@ -541,7 +551,15 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
     a.slots = L.slots;
     a.max_tiles = L.max_tiles;
     a.expert_rows = F;
-    e = qm::launch_gemm(gate->type, qm::GEMM_MOE_GATEUP, a, s);
+    a.C = hf;
+    a.ldc = F;
+    if (fused) {
+      e = qm::launch_gemm(gate->type, qm::GEMM_MOE_GATEUP, a, s);
+    } else {
+      e = qm::launch_gemm(gate->type, qm::GEMM_MOE_G, a, s);
+      a.w = up->view;
+      if (e == hipSuccess) e = qm::launch_gemm(up->type, qm::GEMM_MOE_UH, a, s);
+    }
   }
   if (e == hipSuccess) {
     qm::GemmArgs a{};
@@ -559,8 +577,15 @@ int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_wei
     a.expert_rows = E;
     e = qm::launch_gemm(down->type, qm::GEMM_MOE_DOWN, a, s);
   }
-  if (e == hipSuccess) e = qm::launch_moe_combine(x, y, inv, T, NU, E, accumulate, s);
+  if (e == hipSuccess) e = qm::launch_moe_combine(x, y, inv, T, NU, E, accumulate, shd, s);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
+}
+
+int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
+                        int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,
+                        int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  return qmatmul_moe_grouped_ex(gate, up, down, NE, logits, ldl, T, NU, aq, asc, M_stride, nullptr, nullptr, 0, 0, x,
+                                accumulate, ws, ws_bytes, stream);
 }
 
 

@@ -191,6 +191,65 @@ __device__ __forceinline__ float lane_pick(uint32_t m, float lo, float hi) {
   return __uint_as_float((__float_as_uint(lo) & ~m) | (__float_as_uint(hi) & m));
 }
 
+// Result of an MoE tile mode for slot row `slot` and expert column n of this lane (ok: both in range). Every lane of
+// the wave must call it (the h quantization takes the maximum over the 32 columns of a half-wave):
+//   GEMM_MOE_DOWN: y[slot][n] = routing weight * v
+//   GEMM_MOE_G:    g[slot][n] = v (the gate projection, f32, into C)
+//   GEMM_MOE_GATEUP / GEMM_MOE_UH: h = u * silu(g) (zero/kernels/gemm.cl:464-471) with g = v, u = v2 (one launch) or
+//     g from C, u = v (after a GEMM_MOE_G launch), then quantized per 32 columns -- the wave's 32 columns (lanes of one
+//     half) are one 32-block of the h row -- as moe_quant (zero/kernels/moe.cl:251-282)
+template <int MODE>
+__device__ __forceinline__ void moe_store(const GemmArgs& a, int slot, int n, bool ok, float v, float v2, int lc) {
+  if constexpr (MODE == GEMM_MOE_DOWN) {
+    if (ok) a.C[(size_t)slot * a.ldc + n] = a.rowscale[slot] * v;
+  } else if constexpr (MODE == GEMM_MOE_G) {
+    if (ok) a.C[(size_t)slot * a.ldc + n] = v;
+  } else {
+    float g, u;
+    if constexpr (MODE == GEMM_MOE_GATEUP) {
+      g = v;
+      u = v2;
+    } else {
+      g = ok ? a.C[(size_t)slot * a.ldc + n] : 0.0f;
+      u = v;
+    }
+    const float h = u * (g / (1.0f + expf(-g)));
+    const float amax = max32(fabsf(h));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const int q = (int)__builtin_rintf(h * inv);
+    if (ok) {
+      a.hq[(size_t)slot * a.expert_rows + n] = (int8_t)q;
+      if (lc == 0) a.hsc[(size_t)(n / 32) * a.slots + slot] = amax / 127.0f;
+    }
+  }
+}
+
+// The work-group's rows: a dense M tile, or (MoE modes) one sub-tile of BM slots of an expert's tile of up to
+// kMoeTileRows slots (returns false for work-groups past the tile count or past the tile's rows). wrow0: the
+// expert's first weight row.
+template <int MODE, int BM>
+__device__ __forceinline__ bool tile_rows(const GemmArgs& a, int& m0, int& nvalid, int& wrow0, int& nt) {
+  if constexpr (MODE == GEMM_DENSE) {
+    int mtile;
+    dense_tile(nt, mtile);
+    m0 = mtile * BM;
+    nvalid = min(BM, a.M - m0);
+    wrow0 = 0;
+    return true;
+  } else {
+    constexpr int SUB = kMoeTileRows / BM;
+    const int t = blockIdx.y / SUB, sub = blockIdx.y % SUB;
+    if (t >= a.tiles[0]) return false;
+    const int e = a.tiles[1 + 3 * t];
+    m0 = a.tiles[2 + 3 * t] + sub * BM;
+    nvalid = min(BM, a.tiles[3 + 3 * t] - sub * BM);
+    if (nvalid <= 0) return false;
+    wrow0 = e * a.expert_rows;
+    nt = blockIdx.x;
+    return true;
+  }
+}
+
 template <int TYPE, int MT, int MODE, bool DUMP>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   constexpr int BM = 32 * MT;
@@ -204,24 +263,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
   // ---- which rows: dense (M tile), or one MoE tile (expert e, slots r0 .. r0 + nr - 1)
   int m0, nvalid, wrow0, nt;
-  if constexpr (MODE == GEMM_DENSE) {
-    int mtile;
-    dense_tile(nt, mtile);
-    m0 = mtile * BM;
-    nvalid = min(BM, a.M - m0);
-    wrow0 = 0;
-  } else {
-    // a tile of kMoeTileRows slots is split over kMoeTileRows / BM work-groups
-    constexpr int SUB = kMoeTileRows / BM;
-    const int t = blockIdx.y / SUB, sub = blockIdx.y % SUB;
-    if (t >= a.tiles[0]) return;
-    const int e = a.tiles[1 + 3 * t];
-    m0 = a.tiles[2 + 3 * t] + sub * BM;
-    nvalid = min(BM, a.tiles[3 + 3 * t] - sub * BM);
-    if (nvalid <= 0) return;
-    wrow0 = e * a.expert_rows;
-    nt = blockIdx.x;
-  }
+  if (!tile_rows<MODE, BM>(a, m0, nvalid, wrow0, nt)) return;
   const int n_loc = nt * 128 + wave * 32 + lc;  // this lane's weight row (within the expert)
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
   const int n = wrow0 + min(n_loc, n_rows - 1);
@@ -229,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   if (tid < BM) {
     const int i = min(tid, nvalid - 1);
     int src;
-    if constexpr (MODE == GEMM_MOE_GATEUP) src = a.rowmap[m0 + i];
+    if constexpr (MODE == GEMM_MOE_GATEUP || MODE == GEMM_MOE_G || MODE == GEMM_MOE_UH) src = a.rowmap[m0 + i];
     else src = m0 + i;
     L.arow[tid] = src;
   }
@@ -476,24 +518,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
           }
           *cp = v;
         }
-      } else if constexpr (MODE == GEMM_MOE_DOWN) {
-        if (row_ok && col_ok) {
-          const int slot = m0 + i;
-          a.C[(size_t)slot * a.ldc + n_loc] = a.rowscale[slot] * acc[mt][r];
-        }
       } else {
-        // h = up * silu(gate) (zero/kernels/gemm.cl:464-471), then quantized per 32 columns: the wave's 32 columns
-        // (lanes of one half) are one 32-block of the h row, as moe_quant (zero/kernels/moe.cl:251-282)
-        const float g = acc[mt][r];
-        const float h = acc2[mt][r] * (g / (1.0f + expf(-g)));
-        const float amax = max32(fabsf(h));
-        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-        const int q = (int)__builtin_rintf(h * inv);
-        if (row_ok && col_ok) {
-          const int slot = m0 + i;
-          a.hq[(size_t)slot * a.expert_rows + n_loc] = (int8_t)q;
-          if (lc == 0) a.hsc[(size_t)(n_loc / 32) * a.slots + slot] = amax / 127.0f;
-        }
+        moe_store<MODE>(a, m0 + i, n_loc, row_ok && col_ok, acc[mt][r], GU ? acc2[mt][r] : 0.0f, lc);
       }
     }
   }
@@ -506,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 // signed int8 (Q6_K: the 6-bit value minus 32, a byte-wise subtract without borrows; IQ2: grid words with their
 // signs, groups h and 2 + h of the block); one 2-block f32 outer product gives asc * d * sc for both halves (lanes
 // 0-31: the first half's scale, lanes 32-63: the second's). Tiles, staging and epilogue as gemm_kernel's dense mode.
-template <int TYPE, int MT, bool DUMP>
+template <int TYPE, int MT, int MODE, bool DUMP>
 __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
   constexpr int BM = 32 * MT;
   constexpr int ACH = BM * 16 / 256;
@@ -515,12 +541,15 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
   __shared__ GemmLds<TYPE, MT> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
   const int K = a.w.K, nb = K / 32, nsb = K / 256;
-  int nt, mtile;
-  dense_tile(nt, mtile);
-  const int m0 = mtile * BM, nvalid = min(BM, a.M - m0);
-  const int n_loc = nt * 128 + wave * 32 + lc, n_rows = a.w.rows;
-  const int n = min(n_loc, n_rows - 1);
-  if (tid < BM) L.arow[tid] = m0 + min(tid, nvalid - 1);
+  int m0, nvalid, wrow0, nt;
+  if (!tile_rows<MODE, BM>(a, m0, nvalid, wrow0, nt)) return;
+  const int n_loc = nt * 128 + wave * 32 + lc;
+  const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
+  const int n = wrow0 + min(n_loc, n_rows - 1);
+  if (tid < BM) {
+    const int i = min(tid, nvalid - 1);
+    L.arow[tid] = (MODE == GEMM_MOE_G || MODE == GEMM_MOE_UH) ? a.rowmap[m0 + i] : m0 + i;
+  }
   lds_fill<TYPE>(&L.tab);
   __syncthreads();
 
@@ -669,24 +698,31 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = mt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (i < nvalid && col_ok) {
-        float* cp = a.C + (size_t)(m0 + i) * a.ldc + a.c_off + n_loc;
-        float v = acc[mt][r];
-        if (a.accumulate == 1) {
-          v += *cp;
-        } else if (a.accumulate == 2) {
-          const float g = *cp;
-          v *= g / (1.0f + expf(-g));
+      if constexpr (MODE == GEMM_DENSE) {
+        if (i < nvalid && col_ok) {
+          float* cp = a.C + (size_t)(m0 + i) * a.ldc + a.c_off + n_loc;
+          float v = acc[mt][r];
+          if (a.accumulate == 1) {
+            v += *cp;
+          } else if (a.accumulate == 2) {
+            const float g = *cp;
+            v *= g / (1.0f + expf(-g));
+          }
+          *cp = v;
         }
-        *cp = v;
+      } else {
+        moe_store<MODE>(a, m0 + i, n_loc, i < nvalid && col_ok, acc[mt][r], 0.0f, lc);
       }
     }
 }
 
-template <int TYPE, int MT, bool DUMP>
+template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go_s16(const GemmArgs& a, hipStream_t s) {
-  const unsigned gx = (unsigned)((a.w.rows + 127) / 128), gy = (unsigned)((a.M + 32 * MT - 1) / (32 * MT));
-  gemm_s16_kernel<TYPE, MT, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
+  const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
+  const unsigned gx = (unsigned)((n_rows + 127) / 128);
+  const unsigned gy = MODE == GEMM_DENSE ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT))
+                                          : (unsigned)(a.max_tiles * (kMoeTileRows / (32 * MT)));
+  gemm_s16_kernel<TYPE, MT, MODE, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -709,15 +745,23 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
       return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
     case GEMM_MOE_GATEUP: return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN: return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
+    case GEMM_MOE_G: return go<TYPE, 1, GEMM_MOE_G, false>(a, s);
+    case GEMM_MOE_UH: return go<TYPE, 1, GEMM_MOE_UH, false>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int TYPE>
 static hipError_t dispatch_s16(int mode, const GemmArgs& a, hipStream_t s) {
-  if (mode != GEMM_DENSE) return hipErrorInvalidValue;
-  if (a.dbg_isum) return a.M <= 32 ? go_s16<TYPE, 1, true>(a, s) : go_s16<TYPE, 2, true>(a, s);
-  return a.M <= 32 ? go_s16<TYPE, 1, false>(a, s) : go_s16<TYPE, 2, false>(a, s);
+  if (a.dbg_isum) return a.M <= 32 ? go_s16<TYPE, 1, GEMM_DENSE, true>(a, s) : go_s16<TYPE, 2, GEMM_DENSE, true>(a, s);
+  switch (mode) {
+    case GEMM_DENSE:
+      return a.M <= 32 ? go_s16<TYPE, 1, GEMM_DENSE, false>(a, s) : go_s16<TYPE, 2, GEMM_DENSE, false>(a, s);
+    case GEMM_MOE_G: return go_s16<TYPE, 1, GEMM_MOE_G, false>(a, s);
+    case GEMM_MOE_UH: return go_s16<TYPE, 1, GEMM_MOE_UH, false>(a, s);
+    case GEMM_MOE_DOWN: return go_s16<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
+    default: return hipErrorInvalidValue;  // (gate and up in one launch: the int8 kernel's GATEUP mode only)
+  }
 }
 
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {

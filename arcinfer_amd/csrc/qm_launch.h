@@ -48,7 +48,9 @@ struct GemmArgs {
   int max_tiles;
   int expert_rows;     // rows per expert in w (F for gate/up, E for down)
 };
-enum GemmMode : int { GEMM_DENSE = 0, GEMM_MOE_GATEUP = 1, GEMM_MOE_DOWN = 2 };
+// MoE tile modes: GATEUP (gate and up of one type in one launch: h quantized), G (gate alone: f32 g into C),
+// UH (up alone after G: h from u and g, quantized), DOWN (routing-weighted y)
+enum GemmMode : int { GEMM_DENSE = 0, GEMM_MOE_GATEUP = 1, GEMM_MOE_DOWN = 2, GEMM_MOE_G = 3, GEMM_MOE_UH = 4 };
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s);
 // Prompt GEMM on the f16 matrix pipe (qm_gemm_f16.hip): the types and shapes it takes, its per-call workspace, and
 // the launcher (ws = null: the workspace comes from a per-device stream-ordered pool). dbg_isum: block-sum mode.
@@ -69,18 +71,29 @@ hipError_t launch_add_norm_quant(float* x, const float* t, const float* w, int K
                                  const float* w2, int M, int M_stride, int8_t* aq, float* asc, int16_t* absum,
                                  hipStream_t s);
 
-// MoE routing (qm_moe.hip)
+// The shared expert of an MoE layer: sh [T][ldsh] (null: none), added times g_t = sigmoid(gl[t * ldl]) (gl null:
+// g_t = 1). zero/kernels/moe.cl:332-340, 37-41.
+struct MoeShared {
+  const float* sh;
+  int ldsh;
+  const float* gl;
+  int ldl;
+};
+
+// MoE routing (qm_moe.hip); escale [NE] (or null): each chosen expert's weight times its scale
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
-                            hipStream_t s);
+                            const float* escale, hipStream_t s);
 hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s);
 hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int NE, int* cursor, int* stok,
                               float* swt, int* inv, hipStream_t s);
 hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
-                              hipStream_t s);
+                              const MoeShared& sh, hipStream_t s);
 hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s);
 // MoE at decode sizes (qm_moe_dec.hip): routing + gate/up -> ids, wts, h (f32 [T*NU][F]), then down + combine into x
-hipError_t launch_moe_decode(int type, const WView& gate, const WView& up, const WView& down, int T, int NU, int E,
-                             int F, const float* logits, int ldl, int NE, int* ids, float* wts, const int8_t* aq,
-                             const float* asc, int M_stride, float* h, float* x, int accumulate, hipStream_t s);
+// (gate, up, down of types tg, tu, td; escale: routing expert scales or null; sh: the shared expert or sh.sh null)
+hipError_t launch_moe_decode(int tg, int tu, int td, const WView& gate, const WView& up, const WView& down, int T,
+                             int NU, int E, int F, const float* logits, int ldl, int NE, const float* escale, int* ids,
+                             float* wts, const int8_t* aq, const float* asc, int M_stride, float* h, float* x,
+                             int accumulate, const MoeShared& sh, hipStream_t s);
 
 }  // namespace qm

@@ -14,7 +14,7 @@ namespace qm {
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int ldl, int T, int NE, int NU,
                                                     int tpw, int* __restrict__ ids, float* __restrict__ wts,
-                                                    int* __restrict__ counts) {
+                                                    int* __restrict__ counts, const float* __restrict__ escale) {
   __shared__ int hist[64 * PER_LANE];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (counts)
@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     if (j + 1 < tpw && t + 1 < T) route_load<PER_LANE>(logits + (size_t)(t + 1) * ldl, NE, lane, nv);
     int my_e;
     float my_w;
-    route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w);
+    route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w, escale);
     if (lane < NU) {
       ids[(size_t)t * NU + lane] = my_e;
       wts[(size_t)t * NU + lane] = my_w;
@@ -48,13 +48,13 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 }
 
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
-                            hipStream_t s) {
+                            const float* escale, hipStream_t s) {
   // tokens per wave: enough work-groups to cover the CUs (about 1024 waves), more tokens each for large T
   const int tpw = T >= 2048 ? min(16, T / 1024) : 1;
   const dim3 grid((unsigned)((T + 4 * tpw - 1) / (4 * tpw))), block(256);
-  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
-  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
-  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts);
+  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
+  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
+  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
   return hipGetLastError();
 }
 
@@ -132,10 +132,12 @@ hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, i
   return hipGetLastError();
 }
 
-// x[t][c] (+)= sum_k y[inv[t*NU + k]][c], k in selection order (zero/kernels/moe.cl:332-340). 4 columns per thread.
+// x[t][c] (+)= sum_k y[inv[t*NU + k]][c] (k in selection order) + g_t * sh[t][c] (zero/kernels/moe.cl:332-340):
+// the shared expert's output sh, when given, with its gate g_t = sigmoid(gl[t * ldl]) (gl = the logits' column NE) or
+// 1 without a gate logit. 4 columns per thread.
 __global__ __launch_bounds__(256) void combine_kernel(float* __restrict__ x, const float* __restrict__ y,
                                                       const int* __restrict__ inv, int T, int NU, int E,
-                                                      int accumulate) {
+                                                      int accumulate, MoeShared sh) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int cq = E / 4;
   if (i >= (long)T * cq) return;
@@ -147,6 +149,14 @@ __global__ __launch_bounds__(256) void combine_kernel(float* __restrict__ x, con
     v.y += u.y;
     v.z += u.z;
     v.w += u.w;
+  }
+  if (sh.sh) {
+    const float g = sh.gl ? 1.0f / (1.0f + expf(-sh.gl[(size_t)t * sh.ldl])) : 1.0f;
+    const float4 o = *(const float4*)(sh.sh + (size_t)t * sh.ldsh + c);
+    v.x = v.x + g * o.x;
+    v.y = v.y + g * o.y;
+    v.z = v.z + g * o.z;
+    v.w = v.w + g * o.w;
   }
   float4* xp = (float4*)(x + (size_t)t * E + c);
   if (accumulate) {
@@ -160,9 +170,9 @@ __global__ __launch_bounds__(256) void combine_kernel(float* __restrict__ x, con
 }
 
 hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
-                              hipStream_t s) {
+                              const MoeShared& sh, hipStream_t s) {
   const long n = (long)T * (E / 4);
-  combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, y, inv, T, NU, E, accumulate);
+  combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, y, inv, T, NU, E, accumulate, sh);
   return hipGetLastError();
 }
 

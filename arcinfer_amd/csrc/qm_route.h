@@ -21,8 +21,10 @@ __device__ __forceinline__ void route_load(const float* __restrict__ lg, int NE,
 }
 
 // the selection from the loaded logits (route_load); lane < NU receives the k = lane-th selected expert and its weight
+// (times escale[expert] when escale is non-null: moe.cl:22-28, 75-77, -DESCALE)
 template <int PER_LANE>
-__device__ __forceinline__ void route_select(float (&v)[PER_LANE], int NE, int NU, int lane, int& my_e, float& my_w) {
+__device__ __forceinline__ void route_select(float (&v)[PER_LANE], int NE, int NU, int lane, int& my_e, float& my_w,
+                                             const float* __restrict__ escale = nullptr) {
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < PER_LANE; ++i) mx = fmaxf(mx, v[i]);
@@ -51,23 +53,24 @@ __device__ __forceinline__ void route_select(float (&v)[PER_LANE], int NE, int N
         v[i] = -INFINITY;
         taken |= 1u << i;
       }
-    const float p = expf(gv - mx);
+    const float p = gv > -INFINITY ? expf(gv - mx) : 0.0f;  // (a row of only -inf logits: every weight 0)
     sum += p;
     if (lane == k) {
       my_p = p;
       my_e = gi;
     }
   }
-  my_w = my_p / sum;
+  my_w = sum > 0.0f ? my_p / sum : 0.0f;
+  if (escale && lane < NU) my_w *= escale[my_e];
 }
 
 // lg: the token's NE logits; lane < NU receives the k = lane-th selected expert and its weight
 template <int PER_LANE>
 __device__ __forceinline__ void route_token(const float* __restrict__ lg, int NE, int NU, int lane, int& my_e,
-                                            float& my_w) {
+                                            float& my_w, const float* __restrict__ escale = nullptr) {
   float v[PER_LANE];
   route_load<PER_LANE>(lg, NE, lane, v);
-  route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w);
+  route_select<PER_LANE>(v, NE, NU, lane, my_e, my_w, escale);
 }
 
 }  // namespace qm

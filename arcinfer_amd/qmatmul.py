@@ -33,6 +33,7 @@ SIGNATURES = [
     ("qmatmul_moe_workspace_size", _Z, [_I, _I, _I, _I, _I]),
     ("qmatmul_moe_route", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_moe_grouped", _I, [_P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _Z, _P]),
+    ("qmatmul_moe_grouped_ex", _I, [_P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _I, _P, _Z, _P]),
     ("qmatmul_moe_ws_layout", _I, [_I, _I, _I, _I, _I, _P]),
     ("qmatmul_gemv_blocksums", _I, [_P, _P, _P, _I, _I, _P, _P, _P]),
     ("qmatmul_gemm_blocksums", _I, [_P, _P, _I, _I, _P, _P]),
@@ -222,10 +223,18 @@ def moe_workspace(T, NE, NU, E, F, device="cuda"):
     return torch.empty((n,), dtype=torch.uint8, device=device)
 
 
-def moe_grouped(gate, up, down, NE, logits, NU, aq, asc, x, ws, T=None, accumulate=0, stream=None):
+def moe_grouped(gate, up, down, NE, logits, NU, aq, asc, x, ws, T=None, accumulate=0, stream=None, escale=None,
+                sh=None, sh_gated=True):
+    """qmatmul_moe_grouped, or qmatmul_moe_grouped_ex when escale [NE] or a shared expert's output sh [T, E] is
+    given (sh_gated: gate it with sigmoid(logits[t, NE]), logits then having NE + 1 columns)."""
     T = logits.shape[0] if T is None else T
-    _call("qmatmul_moe_grouped", gate.handle, up.handle, down.handle, NE, _ptr(logits), logits.stride(0), T, NU,
-          _ptr(aq), _ptr(asc), aq.shape[0], _ptr(x), accumulate, _ptr(ws), ws.numel(), _stream(stream))
+    if escale is None and sh is None:
+        _call("qmatmul_moe_grouped", gate.handle, up.handle, down.handle, NE, _ptr(logits), logits.stride(0), T, NU,
+              _ptr(aq), _ptr(asc), aq.shape[0], _ptr(x), accumulate, _ptr(ws), ws.numel(), _stream(stream))
+    else:
+        _call("qmatmul_moe_grouped_ex", gate.handle, up.handle, down.handle, NE, _ptr(logits), logits.stride(0), T,
+              NU, _ptr(aq), _ptr(asc), aq.shape[0], _ptr(escale), _ptr(sh), 0 if sh is None else sh.stride(0),
+              1 if sh_gated else 0, _ptr(x), accumulate, _ptr(ws), ws.numel(), _stream(stream))
     return x
 
 

@@ -144,12 +144,26 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
  * gate, up: NE*F rows of E; down: NE*E rows of F (stacked experts). a_t: token t of aq/asc (E values). q(): the h
  * rows quantized per 32 as moe_quant (moe.cl:251-282). Route, exclusive scan into tiles, device-side scatter of
  * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
- * order (moe.cl:332-340). Gate/up/down types with one integer scale per 32 and no mins (Q8_0, Q4_0, IQ4_NL, IQ4_XS,
- * IQ3_S, IQ2_XXS, IQ3_XXS). accumulate 0 or 1.
+ * order (moe.cl:332-340); at decode sizes (T * NU <= 64) GEMV-shaped expert kernels instead. Gate, up and down each
+ * have their own type, any of Q8_0, Q4_0, IQ4_NL, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, Q6_K -- the types of
+ * the reference's expert GEMM moe_rg (zero/engine_moe.h:297-306); types with per-block mins (Q4_K, Q5_K) return
+ * QM_ERR_TYPE, as there. accumulate 0 or 1.
  * ws: device workspace of at least qmatmul_moe_workspace_size bytes (layout: qmatmul_moe_ws_layout). */
 int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
                         int ldl, int T, int NU, const int8_t* aq, const float* asc, int M_stride, float* x,
                         int accumulate, void* ws, size_t ws_bytes, void* stream);
+
+/* qmatmul_moe_grouped with the routing and combine options of the reference's moe.cl:
+ *   escale [NE] (or NULL): each selected expert's weight, after the normalization over the selection, times
+ *     escale[e] (moe.cl:22-28, 75-77, -DESCALE);
+ *   sh [T][ldsh] (or NULL): the shared expert's output for each token (computed by the caller), added to x as
+ *     x[t] (op)= sum_k w_tk * y_tk + g_t * sh[t], with g_t = sigmoid(logits[t][NE]) when sh_gated (the router's
+ *     extra column: ldl > NE) and g_t = 1 otherwise (moe.cl:37-41, 332-340; -DSH_NOGATE). ldsh >= E, a multiple of 4.
+ * qmatmul_moe_grouped is this call with escale = sh = NULL. */
+int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE,
+                           const float* logits, int ldl, int T, int NU, const int8_t* aq, const float* asc,
+                           int M_stride, const float* escale, const float* sh, int ldsh, int sh_gated, float* x,
+                           int accumulate, void* ws, size_t ws_bytes, void* stream);
 
 /* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). */
 typedef struct {

@@ -58,6 +58,9 @@ def lib():
         _lib.qref_moe_route.argtypes = [P, I, I, I, I, P, P, P]
         _lib.qref_moe_route.restype = None
         _lib.qref_moe_forward.argtypes = [I, P, I, P, I, P, I, I, I, P, I, I, I, P, P, I, P, I, I]
+        _lib.qref_moe_route_ex.argtypes = [P, I, I, I, I, P, P, P, P]
+        _lib.qref_moe_route_ex.restype = None
+        _lib.qref_moe_forward_ex.argtypes = [I, P, I, P, I, P, I, I, I, P, I, I, I, P, P, I, P, P, I, I, P, I, I]
         Fl = ctypes.c_float
         _lib.qref_rmsnorm_quant.argtypes = [P, I, P, I, I, I, Fl, P, P, P, P]
         _lib.qref_rmsnorm_quant.restype = None
@@ -156,26 +159,35 @@ def matmul_f32(qtype, W, K, X, nthreads=0):
     return Y
 
 
-def moe_route(logits, NU, NE=None):
+def moe_route(logits, NU, NE=None, escale=None):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     T, ldl = logits.shape
     NE = ldl if NE is None else NE
     ids = np.empty((T, NU), dtype=np.int32)
     wts = np.empty((T, NU), dtype=np.float32)
     counts = np.empty((NE,), dtype=np.int32)
-    lib().qref_moe_route(_p(logits), ldl, T, NE, NU, _p(ids), _p(wts), _p(counts))
+    esc = None if escale is None else np.ascontiguousarray(escale, dtype=np.float32)
+    lib().qref_moe_route_ex(_p(logits), ldl, T, NE, NU, _p(esc), _p(ids), _p(wts),
+                            _p(counts))
     return ids, wts, counts
 
 
-def moe_forward(tg, Wg, tu, Wu, td, Wd, NE, E, F, logits, NU, aq, asc, x=None, accumulate=False, nthreads=0):
+def moe_forward(tg, Wg, tu, Wu, td, Wd, NE, E, F, logits, NU, aq, asc, x=None, accumulate=False, nthreads=0,
+                escale=None, sh=None, sh_gated=True):
+    """The MoE FFN of qref_moe_forward_ex: logits [T, ldl] (ldl > NE when a gated shared expert is given),
+    escale [NE] or None, sh [T, E] (the shared expert's output) or None."""
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     T = logits.shape[0]
     out = np.zeros((T, E), dtype=np.float32) if x is None else np.ascontiguousarray(x, dtype=np.float32).copy()
     aq = np.ascontiguousarray(aq)
     asc = np.ascontiguousarray(asc, dtype=np.float32)
     Wg, Wu, Wd = (np.ascontiguousarray(w, dtype=np.uint8) for w in (Wg, Wu, Wd))
-    if lib().qref_moe_forward(tg, _p(Wg), tu, _p(Wu), td, _p(Wd), NE, E, F, _p(logits), logits.shape[1], T, NU,
-                              _p(aq), _p(asc), aq.shape[0], _p(out), 1 if accumulate else 0, nthreads):
+    esc = None if escale is None else np.ascontiguousarray(escale, dtype=np.float32)
+    shv = None if sh is None else np.ascontiguousarray(sh, dtype=np.float32)
+    if lib().qref_moe_forward_ex(tg, _p(Wg), tu, _p(Wu), td, _p(Wd), NE, E, F, _p(logits), logits.shape[1], T, NU,
+                                 _p(aq), _p(asc), aq.shape[0], _p(esc),
+                                 _p(shv), E, 1 if sh_gated else 0, _p(out),
+                                 1 if accumulate else 0, nthreads):
         raise ValueError("moe_forward failed")
     return out
 

@@ -455,7 +455,8 @@ int qref_matmul_f32(int type, const uint8_t* W, int N, int K, const float* X, in
 
 /* zero/kernels/moe.cl:42-81 (moe_route): repeated arg-max over the logits (ties: the lower expert), p = exp(l - max)
  * in float, weights p / sum over the selection (sum in selection order) */
-void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts) {
+void qref_moe_route_ex(const float* logits, int ldl, int T, int NE, int NU, const float* escale, int* ids, float* wts,
+                       int* counts) {
   if (counts)
     for (int e = 0; e < NE; ++e) counts[e] = 0;
   char* taken = (char*)malloc((size_t)NE);
@@ -471,29 +472,39 @@ void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* id
         if (!taken[e] && (bi < 0 || l[e] > l[bi])) bi = e;
       taken[bi] = 1;
       ids[(size_t)t * NU + k] = bi;
-      p[k] = expf(l[bi] - mx);
+      /* (a row whose logits are all -inf: every weight 0, the token takes no expert output) */
+      p[k] = l[bi] > -INFINITY ? expf(l[bi] - mx) : 0.0f;
       sum += p[k];
       if (counts) ++counts[bi];
     }
-    for (int k = 0; k < NU; ++k) wts[(size_t)t * NU + k] = p[k] / sum;
+    /* moe.cl:75-77: the normalized weight, times the expert's scale when the model has one (-DESCALE) */
+    for (int k = 0; k < NU; ++k) {
+      const float w = sum > 0.0f ? p[k] / sum : 0.0f;
+      wts[(size_t)t * NU + k] = escale ? w * escale[ids[(size_t)t * NU + k]] : w;
+    }
   }
   free(taken);
 }
 
-int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
-                     const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
-                     const int8_t* aq, const float* asc, int M_stride, float* x, int accumulate, int nthreads) {
+void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts) {
+  qref_moe_route_ex(logits, ldl, T, NE, NU, NULL, ids, wts, counts);
+}
+
+int qref_moe_forward_ex(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
+                        const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
+                        const int8_t* aq, const float* asc, int M_stride, const float* escale, const float* sh,
+                        int ldsh, int sh_gated, float* x, int accumulate, int nthreads) {
   const int sbg = qref_sb_bytes(type_gate), sbu = qref_sb_bytes(type_up), sbd = qref_sb_bytes(type_down);
   if (sbg < 0 || sbu < 0 || sbd < 0 || E % 256 || F % 256 || NU > 64 || T > M_stride) return -1;
   /* (types with per-block mins need the activation sums, which the expert path does not carry: the reference's
-   *  expert GEMM takes no min types either, zero/engine_moe.h:284-289) */
+   *  expert GEMMs take no min types either, zero/engine_moe.h:284-301) */
   if (type_gate == QREF_Q4_K || type_up == QREF_Q4_K || type_down == QREF_Q4_K || type_gate == QREF_Q5_K ||
-      type_up == QREF_Q5_K || type_down == QREF_Q5_K || type_gate == QREF_Q6_K || type_up == QREF_Q6_K ||
-      type_down == QREF_Q6_K)
+      type_up == QREF_Q5_K || type_down == QREF_Q5_K)
     return -1;
+  if (sh && sh_gated && ldl < NE + 1) return -1;
   int* ids = (int*)malloc(sizeof(int) * (size_t)T * NU);
   float* wts = (float*)malloc(sizeof(float) * (size_t)T * NU);
-  qref_moe_route(logits, ldl, T, NE, NU, ids, wts, NULL);
+  qref_moe_route_ex(logits, ldl, T, NE, NU, escale, ids, wts, NULL);
   const size_t rbg = (size_t)(E / 256) * sbg, rbu = (size_t)(E / 256) * sbu, rbd = (size_t)(F / 256) * sbd;
 #ifdef _OPENMP
   if (nthreads <= 0) nthreads = omp_get_max_threads();
@@ -536,10 +547,16 @@ int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_
           y[(size_t)k * E + c] = w * v;
         }
       }
-      /* moe.cl:332-340: the token's NU outputs summed in selection order */
+      /* moe.cl:332-340: the token's NU outputs summed in selection order, plus the shared expert's output times
+       * its gate sigmoid(logits[t][NE]) (moe.cl:37-41; without a gate: times 1) */
+      const float sg = sh ? (sh_gated ? 1.0f / (1.0f + expf(-logits[(size_t)t * ldl + NE])) : 1.0f) : 0.0f;
       for (int c = 0; c < E; ++c) {
         float v = 0.0f;
         for (int k = 0; k < NU; ++k) v += y[(size_t)k * E + c];
+        if (sh) {
+          const float gs = sg * sh[(size_t)t * ldsh + c];
+          v = v + gs;
+        }
         x[(size_t)t * E + c] = accumulate ? x[(size_t)t * E + c] + v : v;
       }
     }
@@ -557,6 +574,13 @@ int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_
   free(ids);
   free(wts);
   return 0;
+}
+
+int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
+                     const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
+                     const int8_t* aq, const float* asc, int M_stride, float* x, int accumulate, int nthreads) {
+  return qref_moe_forward_ex(type_gate, Wg, type_up, Wu, type_down, Wd, NE, E, F, logits, ldl, T, NU, aq, asc,
+                             M_stride, NULL, NULL, 0, 0, x, accumulate, nthreads);
 }
 
 /* ---- activation producers: the kernels that write the path's int8 activations --------------------------------- */

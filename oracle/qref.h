@@ -80,6 +80,9 @@ void qref_add_norm_quant(float* x, const float* t, const float* w, int K, float 
                          int M_stride, int8_t* aq, float* asc, int16_t* absum, float* h);
 
 void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts);
+/* the same, each weight then times escale[expert] when escale is non-null (moe.cl:22-28, 75-77: -DESCALE) */
+void qref_moe_route_ex(const float* logits, int ldl, int T, int NE, int NU, const float* escale, int* ids, float* wts,
+                       int* counts);
 
 /* full MoE FFN on the int8 path (engine_moe.h:8-282, moe.cl:251-340):
  * x[t][E] (+)= sum_k w_k * down_e( quant( silu(gate_e(xq_t)) * up_e(xq_t) ) )
@@ -88,6 +91,13 @@ void qref_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* id
 int qref_moe_forward(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
                      const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
                      const int8_t* aq, const float* asc, int M_stride, float* x, int accumulate, int nthreads);
+/* the same with the expert scales of the routing (escale [NE] or NULL) and a shared expert: sh [T][ldsh] (or NULL)
+ * is added as x[t] += sum_k y_k + g_t * sh[t], g_t = sigmoid(logits[t][NE]) if sh_gated (ldl > NE), else 1
+ * (moe.cl:332-340, 37-41) */
+int qref_moe_forward_ex(int type_gate, const uint8_t* Wg, int type_up, const uint8_t* Wu, int type_down,
+                        const uint8_t* Wd, int NE, int E, int F, const float* logits, int ldl, int T, int NU,
+                        const int8_t* aq, const float* asc, int M_stride, const float* escale, const float* sh,
+                        int ldsh, int sh_gated, float* x, int accumulate, int nthreads);
 
 #ifdef __cplusplus
 }

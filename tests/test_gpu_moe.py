@@ -38,16 +38,18 @@ def test_route_matches_oracle(qm, dev, NE, NU, T):
     assert np.max(np.abs(wts.cpu().numpy() - rw)) < 1e-6
 
 
-def _moe_setup(qm, dev, NE, E, Fd, T, NU, qtype, seed):
+def _moe_setup(qm, dev, NE, E, Fd, T, NU, qtype, seed, types=None, extra_logit=False):
+    """types: (gate, up, down) types, or qtype for all three; extra_logit: a router column NE (shared-expert gate)."""
     import torch
-    Wg = F.synth_weight(qtype, NE * Fd, E, seed=seed, sigma=0.05)
-    Wu = F.synth_weight(qtype, NE * Fd, E, seed=seed + 1, sigma=0.05)
-    Wd = F.synth_weight(qtype, NE * E, Fd, seed=seed + 2, sigma=0.05)
+    tg, tu, td = types if types is not None else (qtype, qtype, qtype)
+    Wg = F.synth_weight(tg, NE * Fd, E, seed=seed, sigma=0.05)
+    Wu = F.synth_weight(tu, NE * Fd, E, seed=seed + 1, sigma=0.05)
+    Wd = F.synth_weight(td, NE * E, Fd, seed=seed + 2, sigma=0.05)
     x = F.synth_activations(T, E, seed=seed + 3)
-    lg = F.zipf_router_logits(T, NE, seed=seed + 4)
+    lg = F.zipf_router_logits(T, NE + (1 if extra_logit else 0), seed=seed + 4)
     xt = to_dev(x, dev)
     aq, asc, absum = qm.quantize_act(xt)
-    g, u, d = (qm.QWeight(qtype, to_dev(W, dev), W.shape[0], K) for W, K in ((Wg, E), (Wu, E), (Wd, Fd)))
+    g, u, d = (qm.QWeight(t, to_dev(W, dev), W.shape[0], K) for t, W, K in ((tg, Wg, E), (tu, Wu, E), (td, Wd, Fd)))
     ws = qm.moe_workspace(T, NE, NU, E, Fd, device=dev)
     out = torch.zeros((T, E), dtype=torch.float32, device=dev)
     return dict(Wg=Wg, Wu=Wu, Wd=Wd, lg=lg, aq=aq, asc=asc, g=g, u=u, d=d, ws=ws, out=out, lgt=to_dev(lg, dev))
@@ -196,3 +198,95 @@ def test_moe_decode_graph_replays(qm, dev, T):
         qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], other, s["ws"])
         torch.cuda.synchronize()
         assert torch.equal(other, eager)
+
+
+# Expert types of the reference's moe_rg beyond the per-32 ones (Q6_K: per-16 int8 scales; IQ2_XS / IQ2_S: per-16
+# 4-bit scales) and gate / up / down of different types, at decode sizes (GEMV-shaped kernels; gate and up of
+# different types as two launches) and prompt sizes (slot tiles; gate-only then up-with-SwiGLU launches), plus the
+# decode kernels' wider configurations (hidden sizes 4096 and 5120: 32 lanes and 4 or 8 blocks per lane; expert width
+# 4096 in the down kernel).
+@pytest.mark.parametrize("types,NE,E,Fd,T,NU", [
+    ((F.Q6_K, F.Q6_K, F.Q6_K), 8, 512, 256, 2, 4), ((F.Q6_K, F.Q6_K, F.Q6_K), 8, 512, 256, 40, 2),
+    ((F.IQ2_XS,) * 3, 8, 512, 256, 3, 4), ((F.IQ2_XS,) * 3, 8, 256, 512, 40, 2),
+    ((F.IQ2_S,) * 3, 16, 512, 256, 2, 4), ((F.IQ2_S,) * 3, 8, 256, 256, 33, 4),
+    ((F.IQ3_S, F.IQ3_S, F.Q6_K), 16, 1024, 512, 1, 8), ((F.IQ3_S, F.IQ3_S, F.Q6_K), 16, 512, 512, 48, 4),
+    ((F.IQ3_S, F.IQ4_XS, F.Q8_0), 8, 512, 256, 4, 4), ((F.IQ3_S, F.IQ4_XS, F.Q8_0), 8, 512, 256, 40, 2),
+    ((F.Q6_K, F.IQ2_S, F.IQ4_XS), 8, 256, 512, 3, 2), ((F.Q6_K, F.IQ2_S, F.IQ4_XS), 8, 256, 512, 64, 2),
+    ((F.IQ4_XS,) * 3, 32, 4096, 512, 1, 8), ((F.IQ4_XS,) * 3, 16, 5120, 256, 4, 4),
+    ((F.IQ4_XS,) * 3, 8, 512, 4096, 2, 4), ((F.IQ4_XS, F.IQ4_XS, F.Q6_K), 8, 512, 4096, 2, 4),
+])
+def test_moe_expert_types_and_mixes(qm, dev, types, NE, E, Fd, T, NU):
+    import torch
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, None, seed=3 * NE + T, types=types)
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    torch.cuda.synchronize()
+    tg, tu, td = types
+    ref = oracle.moe_forward(tg, s["Wg"], tu, s["Wu"], td, s["Wd"], NE, E, Fd, s["lg"], NU, s["aq"].cpu().numpy(),
+                             s["asc"].cpu().numpy())
+    # (per token row: h's int8 requantization per 32 may round one value the other way where the GPU's f32 h and the
+    #  oracle's differ in the last place)
+    assert rel_err(s["out"].cpu().numpy(), ref) < 1e-4
+    for w in (s["g"], s["u"], s["d"]):
+        w.release()
+
+
+@pytest.mark.parametrize("T,NU", [(2, 4), (40, 4)])  # decode sizes / prompt sizes
+@pytest.mark.parametrize("shared", ["gated", "plain", None])
+@pytest.mark.parametrize("escale", [False, True])
+def test_moe_expert_scales_and_shared_expert(qm, dev, T, NU, shared, escale):
+    """moe.cl's options: expert scales on the routing weights (-DESCALE) and the shared expert's output added with
+    its sigmoid gate from the router's column NE (or ungated, -DSH_NOGATE), against the extended oracle."""
+    import torch
+    if shared is None and not escale:
+        pytest.skip("the plain call: covered by the other tests")
+    NE, E, Fd = 16, 512, 256
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=T + NU, extra_logit=True)
+    rng = np.random.default_rng(T)
+    esc = rng.uniform(0.5, 2.0, NE).astype(np.float32) if escale else None
+    sh = rng.standard_normal((T, E)).astype(np.float32) if shared else None
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"],
+                   escale=None if esc is None else to_dev(esc, dev), sh=None if sh is None else to_dev(sh, dev),
+                   sh_gated=shared == "gated")
+    torch.cuda.synchronize()
+    ref = oracle.moe_forward(F.IQ4_XS, s["Wg"], F.IQ4_XS, s["Wu"], F.IQ4_XS, s["Wd"], NE, E, Fd, s["lg"], NU,
+                             s["aq"].cpu().numpy(), s["asc"].cpu().numpy(), escale=esc, sh=sh,
+                             sh_gated=shared == "gated")
+    assert rel_err(s["out"].cpu().numpy(), ref) < 1e-4
+
+
+def test_moe_refuses_min_types_and_checks_the_gate_column(qm, dev):
+    import torch
+    NE, E, Fd, T, NU = 8, 256, 256, 2, 2
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=1)
+    Wk = F.synth_weight(F.Q4_K, NE * Fd, E, seed=2)
+    wk = qm.QWeight(F.Q4_K, to_dev(Wk, dev), NE * Fd, E)
+    with pytest.raises(qm.QMatmulError) as ei:
+        qm.moe_grouped(wk, s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    assert ei.value.status == 3  # QM_ERR_TYPE
+    sh = torch.zeros((T, E), device=dev)
+    with pytest.raises(qm.QMatmulError) as ei:  # (logits have exactly NE columns: no gate logit)
+        qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"], sh=sh)
+    assert ei.value.status == 2  # QM_ERR_SHAPE
+    wk.release()
+
+
+def test_moe_route_fully_masked_row(qm, dev):
+    """A row whose logits are all -inf: the selection is the lowest experts (a stable order) at weight 0, so the
+    token receives no expert output -- on the route launch and on the decode kernel's own routing."""
+    import torch
+    NE, E, Fd, NU = 16, 256, 256, 4
+    for T in (2, 6):
+        s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=T)
+        lg = s["lg"].copy()
+        lg[1, :] = -np.inf
+        lgt = to_dev(lg, dev)
+        ids, wts, _ = qm.moe_route(lgt, NU)
+        torch.cuda.synchronize()
+        assert list(ids.cpu().numpy()[1]) == [0, 1, 2, 3] and np.all(wts.cpu().numpy()[1] == 0.0)
+        qm.moe_grouped(s["g"], s["u"], s["d"], NE, lgt, NU, s["aq"], s["asc"], s["out"], s["ws"])
+        torch.cuda.synchronize()
+        got = s["out"].cpu().numpy()
+        assert np.all(got[1] == 0.0) and np.all(np.isfinite(got))
+        ref = oracle.moe_forward(F.IQ4_XS, s["Wg"], F.IQ4_XS, s["Wu"], F.IQ4_XS, s["Wd"], NE, E, Fd, lg, NU,
+                                 s["aq"].cpu().numpy(), s["asc"].cpu().numpy())
+        assert rel_err(got, ref) < 1e-4

@@ -152,23 +152,43 @@ def test_route_ties_go_to_the_lower_expert():
     assert list(ids[1]) == [3, 9, 12, 0]
 
 
-def test_moe_forward_vs_numpy_pipeline():
+def test_route_expert_scales():
+    """moe.cl:75-77 (-DESCALE): the normalized weight times the chosen expert's scale; the selection is unchanged."""
+    rng = np.random.default_rng(13)
+    lg = rng.standard_normal((9, 32)).astype(np.float32)
+    esc = rng.uniform(0.25, 4.0, 32).astype(np.float32)
+    ids, w, _ = oracle.moe_route(lg, 4)
+    ids2, w2, _ = oracle.moe_route(lg, 4, escale=esc)
+    assert np.array_equal(ids, ids2)
+    assert np.array_equal(w2, (w * esc[ids]).astype(np.float32))
+
+
+@pytest.mark.parametrize("tg,tu,td,escale,shared", [
+    (F.IQ4_XS, F.IQ4_XS, F.IQ4_XS, False, None),
+    (F.IQ3_S, F.IQ4_XS, F.Q6_K, True, "gated"),     # gate, up and down of three types (a GGUF mix)
+    (F.IQ2_XS, F.IQ2_S, F.Q8_0, False, "plain"),    # per-16 integer scales; shared expert without a gate
+])
+def test_moe_forward_vs_numpy_pipeline(tg, tu, td, escale, shared):
     rng = np.random.default_rng(12)
     NE, E, Fd, NU, T = 8, 256, 256, 2, 6
-    t = F.IQ4_XS
-    Wg = F.synth_weight(t, NE * Fd, E, seed=1, sigma=0.05)
-    Wu = F.synth_weight(t, NE * Fd, E, seed=2, sigma=0.05)
-    Wd = F.synth_weight(t, NE * E, Fd, seed=3, sigma=0.05)
+    Wg = F.synth_weight(tg, NE * Fd, E, seed=1, sigma=0.05)
+    Wu = F.synth_weight(tu, NE * Fd, E, seed=2, sigma=0.05)
+    Wd = F.synth_weight(td, NE * E, Fd, seed=3, sigma=0.05)
     x = rng.standard_normal((T, E)).astype(np.float32)
     aq, asc, _ = oracle.quantize_act(x)
-    lg = rng.standard_normal((T, NE)).astype(np.float32)
-    out = oracle.moe_forward(t, Wg, t, Wu, t, Wd, NE, E, Fd, lg, NU, aq, asc)
+    lg = rng.standard_normal((T, NE + 1)).astype(np.float32)  # (column NE: the shared expert's gate logit)
+    esc = rng.uniform(0.5, 2.0, NE).astype(np.float32) if escale else None
+    sh = rng.standard_normal((T, E)).astype(np.float32) if shared else None
+    out = oracle.moe_forward(tg, Wg, tu, Wu, td, Wd, NE, E, Fd, lg, NU, aq, asc, escale=esc, sh=sh,
+                             sh_gated=shared == "gated")
     # numpy pipeline from the pinned pieces: textbook routing, dequantized products in float64, h quantized by the
     # (pinned) quantizer
-    rid, rw = _route_textbook(lg, NU)
-    wg = oracle.dequant_rows(t, Wg, E).astype(np.float64).reshape(NE, Fd, E)
-    wu = oracle.dequant_rows(t, Wu, E).astype(np.float64).reshape(NE, Fd, E)
-    wd = oracle.dequant_rows(t, Wd, Fd).astype(np.float64).reshape(NE, E, Fd)
+    rid, rw = _route_textbook(lg[:, :NE], NU)
+    if escale:
+        rw = rw * esc[rid]
+    wg = oracle.dequant_rows(tg, Wg, E).astype(np.float64).reshape(NE, Fd, E)
+    wu = oracle.dequant_rows(tu, Wu, E).astype(np.float64).reshape(NE, Fd, E)
+    wd = oracle.dequant_rows(td, Wd, Fd).astype(np.float64).reshape(NE, E, Fd)
     xq = aq.astype(np.float64) * np.repeat(asc.T.astype(np.float64), 32, axis=1)
     ref = np.zeros((T, E))
     for ti in range(T):
@@ -180,5 +200,8 @@ def test_moe_forward_vs_numpy_pipeline():
             hq, hs, _ = oracle.quantize_act(h[None])
             hd = hq[0].astype(np.float64) * np.repeat(hs[:, 0].astype(np.float64), 32)
             ref[ti] += rw[ti, k] * (wd[e] @ hd)
+        if shared:
+            g = 1.0 / (1.0 + np.exp(-float(lg[ti, NE]))) if shared == "gated" else 1.0
+            ref[ti] += g * sh[ti]
     err = np.max(np.abs(out - ref)) / np.max(np.abs(ref))
     assert err < 2e-3, err  # (h's int8 requantization may flip a value where float64 and the f32 path differ)
