@@ -237,62 +237,85 @@ int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K) {
   return QM_OK;
 }
 
-int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
-                         void* stream) {
+int qmatmul_quantize_act_ex(const float* x, int ldx, int M, int M_stride, int K, int act32, int8_t* aq, float* asc,
+                            int16_t* absum, void* stream) {
   if (!x || !aq || !asc || !absum) return fail(QM_ERR_ARG, "qmatmul_quantize_act: null pointer");
-  if (K <= 0 || K % 32 || M < 0 || M_stride < 1 || M > M_stride || ldx < K)
-    return fail(QM_ERR_SHAPE, "qmatmul_quantize_act: M %d, M_stride %d, K %d, ldx %d", M, M_stride, K, ldx);
+  if (act32 != 0 && act32 != 1) return fail(QM_ERR_ARG, "qmatmul_quantize_act: act32 %d (0 or 1)", act32);
+  if (K <= 0 || K % (act32 ? 32 : 256) || M < 0 || M_stride < 1 || M > M_stride || ldx < K)
+    return fail(QM_ERR_SHAPE, "qmatmul_quantize_act: M %d, M_stride %d, K %d, ldx %d, act32 %d", M, M_stride, K, ldx,
+                act32);
   if (!aligned(aq, 4)) return fail(QM_ERR_ARG, "qmatmul_quantize_act: aq must be 4-byte aligned");
   QM_CHECK_INIT();
-  const hipError_t e = qm::launch_quantize(x, ldx, M, M_stride, K, aq, asc, absum, (hipStream_t)stream);
+  const hipError_t e = qm::launch_quantize(x, ldx, M, M_stride, K, act32 != 0, aq, asc, absum, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_quantize_act");
 }
 
-static int check_out_acts(const char* fn, int M, int M_stride, int K, const int8_t* aq, const float* asc,
+int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
+                         void* stream) {
+  return qmatmul_quantize_act_ex(x, ldx, M, M_stride, K, 1, aq, asc, absum, stream);
+}
+
+static int check_out_acts(const char* fn, int M, int M_stride, int K, int act32, const int8_t* aq, const float* asc,
                           const int16_t* absum) {
   if (!aq || !asc || !absum) return fail(QM_ERR_ARG, "%s: null output pointer", fn);
-  if (K <= 0 || K % 32 || M < 0 || M_stride < 1 || M > M_stride)
-    return fail(QM_ERR_SHAPE, "%s: M %d, M_stride %d, K %d", fn, M, M_stride, K);
+  if (act32 != 0 && act32 != 1) return fail(QM_ERR_ARG, "%s: act32 %d (0 or 1)", fn, act32);
+  if (K <= 0 || K % (act32 ? 32 : 256) || M < 0 || M_stride < 1 || M > M_stride)
+    return fail(QM_ERR_SHAPE, "%s: M %d, M_stride %d, K %d, act32 %d", fn, M, M_stride, K, act32);
   if (!aligned(aq, 4)) return fail(QM_ERR_ARG, "%s: aq must be 4-byte aligned", fn);
   return QM_OK;
 }
 
-int qmatmul_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
-                          float* asc, int16_t* absum, float* h, int ldh, void* stream) {
-  if (int st = check_out_acts("qmatmul_rmsnorm_quant", M, M_stride, K, aq, asc, absum)) return st;
+int qmatmul_rmsnorm_quant_ex(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int act32,
+                             int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, void* stream) {
+  if (int st = check_out_acts("qmatmul_rmsnorm_quant", M, M_stride, K, act32, aq, asc, absum)) return st;
   if (!x || !w) return fail(QM_ERR_ARG, "qmatmul_rmsnorm_quant: null input");
   if (ldx < K || ldx % 4 || !aligned(x, 16) || !aligned(w, 16) || (h && (ldh < K || ldh % 4 || !aligned(h, 16))))
     return fail(QM_ERR_ARG, "qmatmul_rmsnorm_quant: x, w, h need 16-byte aligned rows (ldx %d, ldh %d, K %d)", ldx,
                 ldh, K);
   QM_CHECK_INIT();
   const hipError_t e = qm::launch_rmsnorm_quant(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh,
-                                                (hipStream_t)stream);
+                                                act32 != 0, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_rmsnorm_quant");
 }
 
-int qmatmul_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
-                         float* asc, int16_t* absum, void* stream) {
-  if (int st = check_out_acts("qmatmul_swiglu_quant", M, M_stride, F, aq, asc, absum)) return st;
+int qmatmul_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int8_t* aq,
+                          float* asc, int16_t* absum, float* h, int ldh, void* stream) {
+  return qmatmul_rmsnorm_quant_ex(x, ldx, w, K, M, M_stride, eps, 1, aq, asc, absum, h, ldh, stream);
+}
+
+int qmatmul_swiglu_quant_ex(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int act32,
+                            int8_t* aq, float* asc, int16_t* absum, void* stream) {
+  if (int st = check_out_acts("qmatmul_swiglu_quant", M, M_stride, F, act32, aq, asc, absum)) return st;
   if (!gu) return fail(QM_ERR_ARG, "qmatmul_swiglu_quant: null input");
   if (ldg < (fused ? F : 2 * F) || ldg % 4 || !aligned(gu, 16))
     return fail(QM_ERR_ARG, "qmatmul_swiglu_quant: ldg %d for F %d (fused %d), 16-byte aligned rows", ldg, F, fused);
   QM_CHECK_INIT();
   const hipError_t e = qm::launch_swiglu_quant(gu, ldg, F, M, M_stride, fused ? 1 : 0, gelu ? 1 : 0, aq, asc, absum,
-                                               (hipStream_t)stream);
+                                               act32 != 0, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_swiglu_quant");
 }
 
-int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
-                           int M_stride, int8_t* aq, float* asc, int16_t* absum, void* stream) {
-  if (int st = check_out_acts("qmatmul_add_norm_quant", M, M_stride, K, aq, asc, absum)) return st;
+int qmatmul_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
+                         float* asc, int16_t* absum, void* stream) {
+  return qmatmul_swiglu_quant_ex(gu, ldg, F, M, M_stride, fused, gelu, 1, aq, asc, absum, stream);
+}
+
+int qmatmul_add_norm_quant_ex(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2,
+                              int M, int M_stride, int act32, int8_t* aq, float* asc, int16_t* absum, void* stream) {
+  if (int st = check_out_acts("qmatmul_add_norm_quant", M, M_stride, K, act32, aq, asc, absum)) return st;
   if (!x || !t || !w) return fail(QM_ERR_ARG, "qmatmul_add_norm_quant: null input");
   if (K > 16384) return fail(QM_ERR_SHAPE, "qmatmul_add_norm_quant: K %d (at most 16384)", K);
   if (!aligned(x, 16) || !aligned(t, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16)))
     return fail(QM_ERR_ARG, "qmatmul_add_norm_quant: x, t, w, w2 must be 16-byte aligned");
   QM_CHECK_INIT();
   const hipError_t e = qm::launch_add_norm_quant(x, t, w, K, eps, s, w2, M, M_stride, aq, asc, absum,
-                                                 (hipStream_t)stream);
+                                                 act32 != 0, (hipStream_t)stream);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_add_norm_quant");
+}
+
+int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
+                           int M_stride, int8_t* aq, float* asc, int16_t* absum, void* stream) {
+  return qmatmul_add_norm_quant_ex(x, t, w, K, eps, s, w2, M, M_stride, 1, aq, asc, absum, stream);
 }
 
 static int check_acts(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
@@ -350,14 +373,20 @@ int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* 
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemv_blocksums");
 }
 
-int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
-                 float* C, int ldc, int c_off, int accumulate, void* stream) {
-  if (int st = check_acts("qmatmul_gemm", w, aq, asc, absum, M, M_stride)) return st;
-  if (!C) return fail(QM_ERR_ARG, "qmatmul_gemm: null output");
-  if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm: rows %d not a multiple of 16", w->rows);
-  if (accumulate < 0 || accumulate > 2) return fail(QM_ERR_ARG, "qmatmul_gemm: accumulate %d (0..2)", accumulate);
+// qmatmul_gemm, qmatmul_gemm_ex and qmatmul_gemm_noalloc: one argument check and dispatch. act32 = 0 takes per-256
+// activation scales (asc [K/256][M_stride]); the kernels then read the scale of 32-block b at row b >> 3.
+static int gemm_impl(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
+                     int M, int M_stride, int act32, float* C, int ldc, int c_off, int accumulate, bool noalloc,
+                     void* stream) {
+  if (int st = check_acts(fn, w, aq, asc, absum, M, M_stride)) return st;
+  if (!C) return fail(QM_ERR_ARG, "%s: null output", fn);
+  if (w->rows % 16) return fail(QM_ERR_SHAPE, "%s: rows %d not a multiple of 16", fn, w->rows);
+  if (accumulate < 0 || accumulate > 2) return fail(QM_ERR_ARG, "%s: accumulate %d (0..2)", fn, accumulate);
   if (c_off < 0 || ldc < c_off + w->rows)
-    return fail(QM_ERR_SHAPE, "qmatmul_gemm: ldc %d, c_off %d, rows %d", ldc, c_off, w->rows);
+    return fail(QM_ERR_SHAPE, "%s: ldc %d, c_off %d, rows %d", fn, ldc, c_off, w->rows);
+  if (act32 != 0 && act32 != 1) return fail(QM_ERR_ARG, "%s: act32 %d (0 or 1)", fn, act32);
+  if (!act32 && w->view.K % 256)
+    return fail(QM_ERR_SHAPE, "%s: per-256 activation scales need K %% 256 == 0 (K %d)", fn, w->view.K);
   QM_CHECK_INIT();
   qm::GemmArgs a{};
   a.w = w->view;
@@ -370,48 +399,41 @@ int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const i
   a.ldc = ldc;
   a.c_off = c_off;
   a.accumulate = accumulate;
-  const hipError_t e = qm::f16_gemm_supported(w->type, M, w->view.K)
-                           ? qm::launch_gemm_f16(w->type, a, nullptr, (hipStream_t)stream)
-                           : qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);
-  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm");
-}
-
-int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
-                         int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream) {
-  if (int st = check_acts("qmatmul_gemm_noalloc", w, aq, asc, absum, M, M_stride)) return st;
-  if (!C) return fail(QM_ERR_ARG, "qmatmul_gemm_noalloc: null output");
-  if (w->rows % 16) return fail(QM_ERR_SHAPE, "qmatmul_gemm_noalloc: rows %d not a multiple of 16", w->rows);
-  if (accumulate < 0 || accumulate > 2)
-    return fail(QM_ERR_ARG, "qmatmul_gemm_noalloc: accumulate %d (0..2)", accumulate);
-  if (c_off < 0 || ldc < c_off + w->rows)
-    return fail(QM_ERR_SHAPE, "qmatmul_gemm_noalloc: ldc %d, c_off %d, rows %d", ldc, c_off, w->rows);
-  QM_CHECK_INIT();
-  qm::GemmArgs a{};
-  a.w = w->view;
-  a.aq = aq;
-  a.asc = asc;
-  a.absum = absum;
-  a.M = M;
-  a.M_stride = M_stride;
-  a.C = C;
-  a.ldc = ldc;
-  a.c_off = c_off;
-  a.accumulate = accumulate;
+  a.ash = act32 ? 0 : 3;
   hipError_t e;
   if (qm::f16_gemm_supported(w->type, M, w->view.K)) {
-    void* scr = nullptr;
-    size_t cap = 0;
-    e = qm::f16_scratch(&scr, &cap);
-    if (e != hipSuccess) return hip_fail(e, "qmatmul_gemm_noalloc: scratch lookup");
-    const size_t need = qm::f16_workspace_bytes(M, w->view.K);
-    if (need > cap)
-      return fail(QM_ERR_WORKSPACE, "qmatmul_gemm_noalloc: M %d x K %d needs %zu bytes of scratch, the static scratch "
-                  "holds %zu (use qmatmul_gemm)", M, w->view.K, need, cap);
+    void* scr = nullptr;  // null: the f16 path takes its workspace from the per-device pool
+    if (noalloc) {
+      size_t cap = 0;
+      e = qm::f16_scratch(&scr, &cap);
+      if (e != hipSuccess) return hip_fail(e, "qmatmul_gemm_noalloc: scratch lookup");
+      const size_t need = qm::f16_workspace_bytes(M, w->view.K);
+      if (need > cap)
+        return fail(QM_ERR_WORKSPACE, "%s: M %d x K %d needs %zu bytes of scratch, the static scratch holds %zu "
+                    "(use qmatmul_gemm)", fn, M, w->view.K, need, cap);
+    }
     e = qm::launch_gemm_f16(w->type, a, scr, (hipStream_t)stream);
   } else {
     e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);  // (this kernel uses no scratch)
   }
-  return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemm_noalloc");
+  return e == hipSuccess ? QM_OK : hip_fail(e, fn);
+}
+
+int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                 float* C, int ldc, int c_off, int accumulate, void* stream) {
+  return gemm_impl("qmatmul_gemm", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, false, stream);
+}
+
+int qmatmul_gemm_ex(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                    int act32, float* C, int ldc, int c_off, int accumulate, void* stream) {
+  return gemm_impl("qmatmul_gemm_ex", w, aq, asc, absum, M, M_stride, act32, C, ldc, c_off, accumulate, false,
+                   stream);
+}
+
+int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
+                         int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream) {
+  return gemm_impl("qmatmul_gemm_noalloc", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, true,
+                   stream);
 }
 
 int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream) {

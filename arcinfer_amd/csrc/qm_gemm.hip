@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     if constexpr (!DUMP) {                                                                                 \
       _Pragma("unroll") for (int c = 0; c < SCH; ++c) {                                                    \
         const int idx = min(tid + 256 * c, 8 * BM - 1), blk = idx / BM, src = L.arow[idx % BM];            \
-        st_sc[c] = a.asc[(size_t)((SB) * 8 + blk) * a.M_stride + src];                                    \
+        st_sc[c] = a.asc[(size_t)(((SB) * 8 + blk) >> a.ash) * a.M_stride + src];                                \
         if constexpr (MINS) {                                                                              \
           const int bs = (int)a.absum[(size_t)(2 * ((SB) * 8 + blk)) * a.M_stride + src] +                 \
                          (int)a.absum[(size_t)(2 * ((SB) * 8 + blk) + 1) * a.M_stride + src];              \
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
 #pragma unroll
       for (int c = 0; c < SCH; ++c) {
         const int idx = min(tid + 256 * c, 8 * BM - 1), blk = idx / BM, src = L.arow[idx % BM];
-        st_sc[c] = a.asc[(size_t)(sb * 8 + blk) * a.M_stride + src];
+        st_sc[c] = a.asc[(size_t)((sb * 8 + blk) >> a.ash) * a.M_stride + src];
       }
     }
   };

@@ -58,7 +58,7 @@ size_t f16_workspace_bytes(int M, int K) {
 // block's two pieces: chunk c = 0 holds elements 8h + perm8(i), chunk 1 elements 16 + 8h + perm8(i).
 template <bool MINS>
 __global__ __launch_bounds__(256) void f16_act_kernel(const int8_t* aq, const float* asc, const int16_t* absum, int M,
-                                                      int M_stride, int Mp, int K, uint8_t* af, uint32_t* u) {
+                                                      int M_stride, int ash, int Mp, int K, uint8_t* af, uint32_t* u) {
   const int nb = K / 32;
   const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
   const int lanei = (int)(gid & 63), h = lanei >> 5;
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void f16_act_kernel(const int8_t* aq, const fl
       float uv = 0.0f;
       if (m < M) {
         const int bs = (int)absum[(size_t)(2 * b) * M_stride + m] + (int)absum[(size_t)(2 * b + 1) * M_stride + m];
-        uv = asc[(size_t)b * M_stride + m] * (float)bs;
+        uv = asc[(size_t)(b >> ash) * M_stride + m] * (float)bs;
       }
       const __bf16 uh = (__bf16)uv;
       const __bf16 ul = (__bf16)(uv - (float)uh);
@@ -112,6 +112,7 @@ struct F16Args {
   const uint32_t* u;   // mins operand
   const float* asc;
   int M, M_stride;
+  int ash;             // asc row of 32-block b: b >> ash (per-32 scales: 0; per-256: 3)
   float* C;
   int ldc, c_off, accumulate;
   int32_t* dbg_isum;   // non-null: write the exact block sums sc * isum [M][rows][K/32] instead of C
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[bb][t] = a.asc[(size_t)(2 * g + bb) * a.M_stride + mrow[t]];
+      for (int t = 0; t < 4; ++t) v[bb][t] = a.asc[(size_t)((2 * g + bb) >> a.ash) * a.M_stride + mrow[t]];
   };
 
   f32x16 tq[4], res[4];
@@ -423,10 +424,10 @@ hipError_t launch_gemm_f16(int type, const GemmArgs& g, void* ws, hipStream_t s)
   // (the block-sum mode reads no activation scales: no mins operand)
   if (g.dbg_isum)
     f16_act_kernel<false><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(g.aq, nullptr, nullptr, M,
-                                                                                       g.M_stride, Mp, K, af, u);
+                                                                                       g.M_stride, 0, Mp, K, af, u);
   else
     f16_act_kernel<true><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(g.aq, g.asc, g.absum, M,
-                                                                                      g.M_stride, Mp, K, af, u);
+                                                                                      g.M_stride, g.ash, Mp, K, af, u);
   e = hipGetLastError();
   if (e == hipSuccess) {
     F16Args a{};
@@ -436,6 +437,7 @@ hipError_t launch_gemm_f16(int type, const GemmArgs& g, void* ws, hipStream_t s)
     a.asc = g.asc;
     a.M = M;
     a.M_stride = g.M_stride;
+    a.ash = g.ash;
     a.C = g.C;
     a.ldc = g.ldc;
     a.c_off = g.c_off;

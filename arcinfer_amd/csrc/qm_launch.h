@@ -11,7 +11,7 @@ namespace qm {
 // GGUF rows -> prepared planes (qm_prep.hip)
 hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t* qs, uint8_t* hdr, hipStream_t s);
 // f32 rows -> int8 + per-32 scales + per-16 sums (qm_prep.hip)
-hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc,
+hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, bool act32, int8_t* aq, float* asc,
                            int16_t* absum, hipStream_t s);
 
 struct GemvArgs {
@@ -38,6 +38,7 @@ struct GemmArgs {
   float* C;
   int ldc, c_off, accumulate;
   int32_t* dbg_isum;
+  int ash = 0;  // activation scales per 32 << ash values: asc row of 32-block b is b >> ash (0, or 3 = per 256)
   // MoE tile mode
   const int* tiles;    // [0] = count, then (expert, first slot, rows) per tile
   const int* rowmap;   // slot -> token (gate/up), or null (down: slot rows)
@@ -64,12 +65,12 @@ constexpr int kMoeTileRows = 32;
 
 // Activation producers (qm_producers.hip)
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps,
-                                int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, hipStream_t s);
+                                int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, bool act32, hipStream_t s);
 hipError_t launch_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
-                               float* asc, int16_t* absum, hipStream_t s);
+                               float* asc, int16_t* absum, bool act32, hipStream_t s);
 hipError_t launch_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float scale,
                                  const float* w2, int M, int M_stride, int8_t* aq, float* asc, int16_t* absum,
-                                 hipStream_t s);
+                                 bool act32, hipStream_t s);
 
 // The shared expert of an MoE layer: sh [T][ldsh] (null: none), added times g_t = sigmoid(gl[t * ldl]) (gl null:
 // g_t = 1). zero/kernels/moe.cl:332-340, 37-41.

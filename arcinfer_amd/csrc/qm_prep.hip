@@ -174,7 +174,10 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t*
 // Activation quantizer: 8 lanes per 32-block, 4 values per lane. amax is combined over the 8 lanes (max is
 // order-free), then each value is rounded on its own: q = rint(v * (127 / amax)) with IEEE division and
 // round-half-even, the expression of quantize_act_cpu (src/quants.h:559-576) -- bit-exact. Rows m >= M (up to
-// M_stride) are written as zero rows with scale 0.
+// M_stride) are written as zero rows with scale 0. A32 = false: one scale per 256 values (quantize_act_cpu with
+// act32 = false, asc [K/256][M_stride]); a superblock's 64 lanes are one whole wave (K % 256 == 0), so amax is the
+// wave maximum.
+template <bool A32>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int ldx, int M, int M_stride,
                                                        int K, int8_t* __restrict__ aq, float* __restrict__ asc,
                                                        int16_t* __restrict__ absum) {
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     for (int i = 0; i < 4; ++i) v[i] = src[i];
   }
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = max8(amax);
+  amax = A32 ? max8(amax) : wave_max(amax);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int sum = 0;
   uint32_t pk = 0;
@@ -205,15 +208,16 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
   sum = sum4_i(sum);
   if (!live) return;
   *(uint32_t*)(aq + (size_t)m * K + 32 * b + 4 * sub) = pk;
-  if (sub == 0) asc[(size_t)b * M_stride + m] = amax / 127.0f;
+  if (A32 ? sub == 0 : (sub == 0 && (b & 7) == 0)) asc[(size_t)(A32 ? b : b >> 3) * M_stride + m] = amax / 127.0f;
   if ((sub & 3) == 0) absum[(size_t)(2 * b + (sub >> 2)) * M_stride + m] = (int16_t)sum;
 }
 
-hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc,
+hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, bool act32, int8_t* aq, float* asc,
                            int16_t* absum, hipStream_t s) {
   const long lanes = (long)M_stride * (K / 32) * 8;
   const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
-  quantize_kernel<<<grid, block, 0, s>>>(x, ldx, M, M_stride, K, aq, asc, absum);
+  if (act32) quantize_kernel<true><<<grid, block, 0, s>>>(x, ldx, M, M_stride, K, aq, asc, absum);
+  else quantize_kernel<false><<<grid, block, 0, s>>>(x, ldx, M, M_stride, K, aq, asc, absum);
   return hipGetLastError();
 }
 

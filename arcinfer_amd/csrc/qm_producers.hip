@@ -9,12 +9,14 @@ namespace qm {
 namespace {
 
 // Quantizes one 32-block held by 8 consecutive lanes (lane `sub` holds elements 4*sub .. 4*sub+3). Every lane of the
-// wave calls it (the shuffles); `store` masks the writes.
+// wave calls it (the shuffles); `store` masks the writes. a32 = 0: one scale per 256 values (asc [K/256][M_stride]);
+// every caller gives wave w the blocks 8w .. 8w+7 of a 32-block-aligned pass, i.e. one whole superblock, so its amax
+// is the wave maximum.
 __device__ __forceinline__ void quant8(const float v[4], int sub, bool store, int m, int b, int M_stride, int K,
                                        int8_t* __restrict__ aq, float* __restrict__ asc,
-                                       int16_t* __restrict__ absum) {
+                                       int16_t* __restrict__ absum, int a32) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = max8(amax);
+  amax = a32 ? max8(amax) : wave_max(amax);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int sum = 0;
   uint32_t pk = 0;
@@ -27,7 +29,7 @@ __device__ __forceinline__ void quant8(const float v[4], int sub, bool store, in
   sum = sum4_i(sum);
   if (!store) return;
   *(uint32_t*)(aq + (size_t)m * K + 32 * b + 4 * sub) = pk;
-  if (sub == 0) asc[(size_t)b * M_stride + m] = amax / 127.0f;
+  if (sub == 0 && (a32 || (b & 7) == 0)) asc[(size_t)(a32 ? b : b >> 3) * M_stride + m] = amax / 127.0f;
   if ((sub & 3) == 0) absum[(size_t)(2 * b + (sub >> 2)) * M_stride + m] = (int16_t)sum;
 }
 
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
                                                             const float* __restrict__ w, int K, int M, int M_stride,
                                                             float eps, int8_t* __restrict__ aq,
                                                             float* __restrict__ asc, int16_t* __restrict__ absum,
-                                                            float* __restrict__ h, int ldh) {
+                                                            float* __restrict__ h, int ldh, int a32) {
   __shared__ float red[4];
   const int m = blockIdx.x, nb = K / 32, sub = threadIdx.x & 7;
   const bool valid = m < M;
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
       v[3] = xv.w * r * wv.w;
     }
     if (h && live) *(float4*)(h + (size_t)m * ldh + 32 * b + 4 * sub) = make_float4(v[0], v[1], v[2], v[3]);
-    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum);
+    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum, a32);
   }
 }
 
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int ldg, int F, int M,
                                                            int M_stride, int fused, int gelu,
                                                            int8_t* __restrict__ aq, float* __restrict__ asc,
-                                                           int16_t* __restrict__ absum) {
+                                                           int16_t* __restrict__ absum, int a32) {
   const int m = blockIdx.x, nb = F / 32, sub = threadIdx.x & 7;
   const bool valid = m < M;
   const float* g = gu + (size_t)m * ldg;
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
         for (int i = 0; i < 4; ++i) v[i] = (gelu ? gelu_tanh(ga[i]) : silu(ga[i])) * ua[i];
       }
     }
-    quant8(v, sub, live, m, b, M_stride, F, aq, asc, absum);
+    quant8(v, sub, live, m, b, M_stride, F, aq, asc, absum, a32);
   }
 }
 
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_reg_kernel(const float* __r
                                                                 const float* __restrict__ w, int K, int M,
                                                                 int M_stride, float eps, int8_t* __restrict__ aq,
                                                                 float* __restrict__ asc, int16_t* __restrict__ absum,
-                                                                float* __restrict__ h, int ldh) {
+                                                                float* __restrict__ h, int ldh, int a32) {
   __shared__ float red[4];
   const int m = blockIdx.x, c = blockIdx.y, nb = K / 32, sub = threadIdx.x & 7;
   const bool valid = m < M;
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_reg_kernel(const float* __r
       v[3] = xv[p].w * r * wv.w;
     }
     if (h && live) *(float4*)(h + (size_t)m * ldh + 32 * b + 4 * sub) = make_float4(v[0], v[1], v[2], v[3]);
-    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum);
+    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum, a32);
   }
 }
 
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(256) void add_norm_quant_kernel(float* __restrict__
                                                              const float* __restrict__ w, int K, float eps, float s,
                                                              const float* __restrict__ w2, int M, int M_stride,
                                                              int8_t* __restrict__ aq, float* __restrict__ asc,
-                                                             int16_t* __restrict__ absum) {
+                                                             int16_t* __restrict__ absum, int a32) {
   __shared__ float red[4];
   const int m = blockIdx.x, nb = K / 32, sub = threadIdx.x & 7;
   const bool valid = m < M;
@@ -241,38 +243,41 @@ __global__ __launch_bounds__(256) void add_norm_quant_kernel(float* __restrict__
       v[2] = xv[p][2] * r2 * w4.z;
       v[3] = xv[p][3] * r2 * w4.w;
     }
-    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum);
+    quant8(v, sub, live, m, b, M_stride, K, aq, asc, absum, a32);
   }
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps,
-                                int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, hipStream_t s) {
+                                int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, bool act32, hipStream_t s) {
+  const int a32 = act32 ? 1 : 0;
   const int passes = (K / 32 + 31) / 32;
   const unsigned split = M_stride < 256 ? (unsigned)passes : 1u;  // (few rows: the GPU would be nearly idle)
-#define QM_RNQ(P) rmsnorm_quant_reg_kernel<P><<<dim3(M_stride, split), 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh)
+#define QM_RNQ(P) rmsnorm_quant_reg_kernel<P><<<dim3(M_stride, split), 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh, a32)
   if (passes <= 1) QM_RNQ(1);
   else if (passes <= 2) QM_RNQ(2);
   else if (passes <= 4) QM_RNQ(4);
   else if (passes <= 8) QM_RNQ(8);
   else if (passes <= 16) QM_RNQ(16);
-  else rmsnorm_quant_kernel<<<M_stride, 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh);
+  else rmsnorm_quant_kernel<<<M_stride, 256, 0, s>>>(x, ldx, w, K, M, M_stride, eps, aq, asc, absum, h, ldh, a32);
 #undef QM_RNQ
   return hipGetLastError();
 }
 
 hipError_t launch_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int8_t* aq,
-                               float* asc, int16_t* absum, hipStream_t s) {
+                               float* asc, int16_t* absum, bool act32, hipStream_t s) {
+  const int a32 = act32 ? 1 : 0;
   // one work-group per row and chunk of 32 blocks (1024 values): a decode row of F = 17408 spreads over 17
   const unsigned chunks = (unsigned)((F / 32 + 31) / 32);
-  swiglu_quant_kernel<<<dim3(M_stride, chunks), 256, 0, s>>>(gu, ldg, F, M, M_stride, fused, gelu, aq, asc, absum);
+  swiglu_quant_kernel<<<dim3(M_stride, chunks), 256, 0, s>>>(gu, ldg, F, M, M_stride, fused, gelu, aq, asc, absum, a32);
   return hipGetLastError();
 }
 
 hipError_t launch_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float scale,
                                  const float* w2, int M, int M_stride, int8_t* aq, float* asc, int16_t* absum,
-                                 hipStream_t s) {
+                                 bool act32, hipStream_t s) {
+  const int a32 = act32 ? 1 : 0;
   const int passes = (K / 32 + 31) / 32;
-#define QM_ANQ(P) add_norm_quant_kernel<P><<<M_stride, 256, 0, s>>>(x, t, w, K, eps, scale, w2, M, M_stride, aq, asc, absum)
+#define QM_ANQ(P) add_norm_quant_kernel<P><<<M_stride, 256, 0, s>>>(x, t, w, K, eps, scale, w2, M, M_stride, aq, asc, absum, a32)
   if (passes <= 1) QM_ANQ(1);
   else if (passes <= 2) QM_ANQ(2);
   else if (passes <= 4) QM_ANQ(4);

@@ -27,8 +27,10 @@ SIGNATURES = [
     ("qmatmul_release_weight", _I, [_P]),
     ("qmatmul_weight_info", _I, [_P, _c.POINTER(_I), _c.POINTER(_I), _c.POINTER(_I)]),
     ("qmatmul_quantize_act", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_quantize_act_ex", _I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_gemv", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_gemm", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    ("qmatmul_gemm_ex", _I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_gemm_noalloc", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_moe_workspace_size", _Z, [_I, _I, _I, _I, _I]),
     ("qmatmul_moe_route", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
@@ -40,6 +42,9 @@ SIGNATURES = [
     ("qmatmul_rmsnorm_quant", _I, [_P, _I, _P, _I, _I, _I, _c.c_float, _P, _P, _P, _P, _I, _P]),
     ("qmatmul_swiglu_quant", _I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_add_norm_quant", _I, [_P, _P, _P, _I, _c.c_float, _c.c_float, _P, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_rmsnorm_quant_ex", _I, [_P, _I, _P, _I, _I, _I, _c.c_float, _I, _P, _P, _P, _P, _I, _P]),
+    ("qmatmul_swiglu_quant_ex", _I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    ("qmatmul_add_norm_quant_ex", _I, [_P, _P, _P, _I, _c.c_float, _c.c_float, _P, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_gguf_open", _I, [_c.c_char_p, _c.POINTER(_P)]),
     ("qmatmul_gguf_close", _I, [_P]),
     ("qmatmul_gguf_tensor_count", _I, [_P, _c.POINTER(_I)]),
@@ -146,15 +151,17 @@ class QWeight:
             pass
 
 
-def quantize_act(x, M_stride=None, stream=None):
-    """x f32 [M, K] (cuda) -> (aq int8 [M_stride, K], asc f32 [K/32, M_stride], absum int16 [K/16, M_stride])."""
-    import torch
+def quantize_act(x, M_stride=None, stream=None, act32=True):
+    """x f32 [M, K] (cuda) -> (aq int8 [M_stride, K], asc f32 [K/32, M_stride], absum int16 [K/16, M_stride]);
+    act32=False: per-256 scales, asc [K/256, M_stride] (qmatmul_quantize_act_ex)."""
     M, K = x.shape
     Ms = M if M_stride is None else M_stride
-    aq = torch.empty((Ms, K), dtype=torch.int8, device=x.device)
-    asc = torch.empty((K // 32, Ms), dtype=torch.float32, device=x.device)
-    absum = torch.empty((K // 16, Ms), dtype=torch.int16, device=x.device)
-    _call("qmatmul_quantize_act", _ptr(x), x.stride(0), M, Ms, K, _ptr(aq), _ptr(asc), _ptr(absum), _stream(stream))
+    aq, asc, absum = _out_acts(Ms, K, x.device, act32)
+    if act32:
+        _call("qmatmul_quantize_act", _ptr(x), x.stride(0), M, Ms, K, _ptr(aq), _ptr(asc), _ptr(absum), _stream(stream))
+    else:
+        _call("qmatmul_quantize_act_ex", _ptr(x), x.stride(0), M, Ms, K, 0, _ptr(aq), _ptr(asc), _ptr(absum),
+              _stream(stream))
     return aq, asc, absum
 
 
@@ -169,14 +176,21 @@ def gemv(w, aq, asc, absum, T=1, C=None, ldc=None, c_off=0, accumulate=0, stream
     return C
 
 
-def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None, noalloc=False):
-    """qmatmul_gemm (noalloc=True: qmatmul_gemm_noalloc, the entry point that allocates no device memory)."""
+def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None, noalloc=False, act32=True):
+    """qmatmul_gemm (noalloc=True: qmatmul_gemm_noalloc, the entry point that allocates no device memory;
+    act32=False: qmatmul_gemm_ex with per-256 activation scales)."""
     import torch
     Ms = aq.shape[0]
     M = Ms if M is None else M
     if C is None:
         C = torch.empty((M, w.rows), dtype=torch.float32, device=aq.device)
         ldc = w.rows
+    if not act32:
+        if noalloc:
+            raise ValueError("qmatmul_gemm_noalloc takes per-32 activation scales only")
+        _call("qmatmul_gemm_ex", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, 0, _ptr(C),
+              w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
+        return C
     _call("qmatmul_gemm_noalloc" if noalloc else "qmatmul_gemm", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, _ptr(C),
           w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
     return C
@@ -238,40 +252,41 @@ def moe_grouped(gate, up, down, NE, logits, NU, aq, asc, x, ws, T=None, accumula
     return x
 
 
-def _out_acts(Ms, K, dev):
+def _out_acts(Ms, K, dev, act32=True):
     import torch
-    return (torch.empty((Ms, K), dtype=torch.int8, device=dev), torch.empty((K // 32, Ms), dtype=torch.float32, device=dev),
+    return (torch.empty((Ms, K), dtype=torch.int8, device=dev),
+            torch.empty((K // (32 if act32 else 256), Ms), dtype=torch.float32, device=dev),
             torch.empty((K // 16, Ms), dtype=torch.int16, device=dev))
 
 
-def rmsnorm_quant(x, w, eps, M_stride=None, want_h=False, stream=None):
-    """x f32 [M, K] (cuda), w [K] -> (aq, asc, absum, h or None)."""
+def rmsnorm_quant(x, w, eps, M_stride=None, want_h=False, stream=None, act32=True):
+    """x f32 [M, K] (cuda), w [K] -> (aq, asc, absum, h or None); act32=False: per-256 scales."""
     import torch
     M, K = x.shape
     Ms = M if M_stride is None else M_stride
-    aq, asc, absum = _out_acts(Ms, K, x.device)
+    aq, asc, absum = _out_acts(Ms, K, x.device, act32)
     h = torch.empty((Ms, K), dtype=torch.float32, device=x.device) if want_h else None
-    _call("qmatmul_rmsnorm_quant", _ptr(x), x.stride(0), _ptr(w), K, M, Ms, float(eps), _ptr(aq), _ptr(asc),
-          _ptr(absum), _ptr(h), K, _stream(stream))
+    _call("qmatmul_rmsnorm_quant_ex", _ptr(x), x.stride(0), _ptr(w), K, M, Ms, float(eps), int(act32), _ptr(aq),
+          _ptr(asc), _ptr(absum), _ptr(h), K, _stream(stream))
     return aq, asc, absum, h
 
 
-def swiglu_quant(gu, F, fused=False, gelu=False, M_stride=None, stream=None):
+def swiglu_quant(gu, F, fused=False, gelu=False, M_stride=None, stream=None, act32=True):
     M = gu.shape[0]
     Ms = M if M_stride is None else M_stride
-    aq, asc, absum = _out_acts(Ms, F, gu.device)
-    _call("qmatmul_swiglu_quant", _ptr(gu), gu.stride(0), F, M, Ms, int(fused), int(gelu), _ptr(aq), _ptr(asc),
-          _ptr(absum), _stream(stream))
+    aq, asc, absum = _out_acts(Ms, F, gu.device, act32)
+    _call("qmatmul_swiglu_quant_ex", _ptr(gu), gu.stride(0), F, M, Ms, int(fused), int(gelu), int(act32), _ptr(aq),
+          _ptr(asc), _ptr(absum), _stream(stream))
     return aq, asc, absum
 
 
-def add_norm_quant(x, t, w, eps, s, w2=None, M_stride=None, stream=None):
+def add_norm_quant(x, t, w, eps, s, w2=None, M_stride=None, stream=None, act32=True):
     """Updates x in place; returns (aq, asc, absum)."""
     M, K = x.shape
     Ms = M if M_stride is None else M_stride
-    aq, asc, absum = _out_acts(Ms, K, x.device)
-    _call("qmatmul_add_norm_quant", _ptr(x), _ptr(t), _ptr(w), K, float(eps), float(s), _ptr(w2), M, Ms, _ptr(aq),
-          _ptr(asc), _ptr(absum), _stream(stream))
+    aq, asc, absum = _out_acts(Ms, K, x.device, act32)
+    _call("qmatmul_add_norm_quant_ex", _ptr(x), _ptr(t), _ptr(w), K, float(eps), float(s), _ptr(w2), M, Ms,
+          int(act32), _ptr(aq), _ptr(asc), _ptr(absum), _stream(stream))
     return aq, asc, absum
 
 

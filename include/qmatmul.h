@@ -11,6 +11,10 @@
  *   asc   float [K/32][M_stride] scale of each 32-block, token fastest
  *   absum int16 [K/16][M_stride] sum of each 16-block's int8 values, token fastest (needed by Q4_K only)
  * Rows M..M_stride-1 of a padded batch are zero rows.
+ * The per-256 layout (act32 = 0 in the reference: Engine::matmul's act32 flag, zero/engine.h:3151, 3300, and
+ * quantize_act_cpu with B = 256, src/quants.h:559-576) has asc float [K/256][M_stride], one scale per 256 values;
+ * it is written by the *_ex producers and the quantizer with act32 = 0 and read by qmatmul_gemm_ex with act32 = 0
+ * (the reference uses it only for prompt GEMMs: every GEMV and MoE input is per-32, zero/engine.h:3300).
  *
  * Weights: GGUF blocks, rows of K elements, K a multiple of 256 (Q8_0: 8 blocks of 32 per 256). A weight is
  * prepared once (qmatmul_prepare_weight) into this library's own device layout and then read by every product.
@@ -81,6 +85,10 @@ int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K);
  * (zero/engine.h:3302-3308, 3451-3456). K % 32 == 0. */
 int qmatmul_quantize_act(const float* x, int ldx, int M, int M_stride, int K, int8_t* aq, float* asc, int16_t* absum,
                          void* stream);
+/* The same with the reference's act32 flag: act32 = 1 is qmatmul_quantize_act; act32 = 0 takes amax over each 256
+ * values and writes asc [K/256][M_stride] (K % 256 == 0), bit-exact with quantize_act_cpu(act32 = false). */
+int qmatmul_quantize_act_ex(const float* x, int ldx, int M, int M_stride, int K, int act32, int8_t* aq, float* asc,
+                            int16_t* absum, void* stream);
 
 /* Producers of the activations (the step before every product), fused with the quantizer above (act32 layout):
  *
@@ -101,6 +109,15 @@ int qmatmul_swiglu_quant(const float* gu, int ldg, int F, int M, int M_stride, i
                          float* asc, int16_t* absum, void* stream);
 int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2, int M,
                            int M_stride, int8_t* aq, float* asc, int16_t* absum, void* stream);
+/* The three producers with the reference's act32 argument (Engine::rmsnorm_quant / add_norm_quant / quant_rows,
+ * zero/engine.h:3302, 3415, 3451): act32 = 1 is the functions above; act32 = 0 writes per-256 scales
+ * (asc [K/256][M_stride], K % 256 == 0). */
+int qmatmul_rmsnorm_quant_ex(const float* x, int ldx, const float* w, int K, int M, int M_stride, float eps, int act32,
+                             int8_t* aq, float* asc, int16_t* absum, float* h, int ldh, void* stream);
+int qmatmul_swiglu_quant_ex(const float* gu, int ldg, int F, int M, int M_stride, int fused, int gelu, int act32,
+                            int8_t* aq, float* asc, int16_t* absum, void* stream);
+int qmatmul_add_norm_quant_ex(float* x, const float* t, const float* w, int K, float eps, float s, const float* w2,
+                              int M, int M_stride, int act32, int8_t* aq, float* asc, int16_t* absum, void* stream);
 
 /* Decode GEMV, T tokens (1..8) against one read of the weight:
  *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
@@ -118,6 +135,13 @@ int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const i
  * from a per-device stream-ordered memory pool; every other case runs on int8 MFMA and allocates nothing. */
 int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                  float* C, int ldc, int c_off, int accumulate, void* stream);
+/* qmatmul_gemm with the act32 argument of Engine::matmul / matmul1 (zero/engine.h:3151, 3184, 3247; gemm.cl built
+ * with or without -DACT32): act32 = 1 is qmatmul_gemm; act32 = 0 reads per-256 activation scales (asc [K/256][M_stride],
+ * K % 256 == 0) -- the same kernels, which then take the scale of 32-block b from row b / 8. The per-256 result
+ * equals the reference's superblock form asc * (d * sum_b sc*isum - dmin * sum_b mn*bsum) (gemm.cl:413-447) up to
+ * f32 rounding order. */
+int qmatmul_gemm_ex(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                    int act32, float* C, int ldc, int c_off, int accumulate, void* stream);
 
 /* qmatmul_gemm without any device allocation. No counterpart in the reference: for callers that cannot allocate
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same arguments, results and kernels

@@ -149,6 +149,16 @@ def blockdot(qtype, W, K, aq, asc, absum, M=None, blocksums=False, col_stride=1,
     return (C, isum, msum) if blocksums else C
 
 
+def blockdot256(qtype, W, K, aq, asc256, absum, M=None, col_stride=1, nthreads=0):
+    """The product with per-256 activation scales (the reference's act32 = false GEMM, zero/kernels/gemm.cl:413-447:
+    per superblock res += asc * (d * sum_b sc*isum) - asc * (dmin * sum_b mn*bsum)). Every 32-block of a
+    superblock carries the superblock's scale, so in qref_blockdot's double accumulation the per-block form
+    sum_b asc * d * (sc*isum) equals the reference's superblock form exactly; this expands asc [K/256][M_stride] to
+    the per-32 layout and calls it."""
+    asc32 = np.repeat(np.ascontiguousarray(asc256, dtype=np.float32), 8, axis=0)
+    return blockdot(qtype, W, K, aq, asc32, absum, M=M, col_stride=col_stride, nthreads=nthreads)
+
+
 def matmul_f32(qtype, W, K, X, nthreads=0):
     W = np.ascontiguousarray(W, dtype=np.uint8)
     X = np.ascontiguousarray(X, dtype=np.float32)

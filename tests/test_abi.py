@@ -52,5 +52,9 @@ def test_argument_errors_need_no_gpu(qm):
     assert lib.qmatmul_prepare_weight(23, buf, 0, 16, 100, None, ctypes.byref(h)) == 2
     assert lib.qmatmul_gemv(None, None, None, None, 1, 1, None, 0, 0, 0, None) == 1
     assert lib.qmatmul_quantize_act(buf, 32, 1, 1, 33, buf, buf, buf, None) == 2
+    # per-256 activation scales (act32 = 0) need K % 256 == 0; act32 is 0 or 1
+    assert lib.qmatmul_quantize_act_ex(buf, 288, 1, 1, 288, 0, buf, buf, buf, None) == 2
+    assert lib.qmatmul_quantize_act_ex(buf, 256, 1, 1, 256, 2, buf, buf, buf, None) == 1
+    assert lib.qmatmul_swiglu_quant_ex(buf, 576, 288, 1, 1, 0, 0, 0, buf, buf, buf, None) == 2
     with pytest.raises(qm.QMatmulError):
         qm._call("qmatmul_moe_ws_layout", 0, 1, 1, 1, 1, None)

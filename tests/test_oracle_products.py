@@ -112,6 +112,58 @@ def test_blockdot_f32_vs_dequantized_double(qtype):
     assert np.max(np.abs(Y - ref)) / np.max(np.abs(ref)) < 1e-6
 
 
+def test_quantize_per256_scales():
+    """act32 = false (quantize_act_cpu with B = 256): one amax per 256 values. Where every 32-block of a superblock
+    has the superblock's amax, the result is the per-32 one with each scale repeated; the element at amax maps to
+    +-127; rows past M are zero; absum stays per 16."""
+    rng = np.random.default_rng(5)
+    M, Ms, K = 3, 4, 1024
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    for m in range(M):
+        for s_ in range(K // 256):
+            a = np.float32(rng.uniform(0.5, 40))
+            x[m, 256 * s_: 256 * s_ + 256] = np.clip(x[m, 256 * s_: 256 * s_ + 256], -a, a)
+            x[m, 256 * s_: 256 * s_ + 256: 32] = a  # every 32-block holds the superblock's amax
+    q256, s256, a256 = oracle.quantize_act(x, M_stride=Ms, act32=False)
+    q32, s32, a32 = oracle.quantize_act(x, M_stride=Ms)
+    assert s256.shape == (K // 256, Ms) and a256.shape == (K // 16, Ms)
+    assert np.array_equal(q256, q32) and np.array_equal(a256, a32)
+    assert np.array_equal(np.repeat(s256, 8, axis=0), s32)
+    # general rows: the scale is max |x| over the 256 values / 127, and that element maps to +-127
+    y = rng.standard_normal((2, 512)).astype(np.float32) * np.float32(3)
+    y[1, 256:512] = 0
+    q, sc, ab = oracle.quantize_act(y, act32=False)
+    for m in range(2):
+        for s_ in range(2):
+            seg = y[m, 256 * s_: 256 * s_ + 256]
+            amax = np.max(np.abs(seg))
+            assert sc[s_, m] == np.float32(amax) / np.float32(127)
+            if amax > 0:
+                i = int(np.argmax(np.abs(seg)))
+                assert abs(int(q[m, 256 * s_ + i])) == 127
+                inv = np.float32(127) / np.float32(amax)
+                assert np.array_equal(q[m, 256 * s_: 256 * s_ + 256], np.rint(seg * inv).astype(np.int8))
+            else:
+                assert np.all(q[m, 256 * s_: 256 * s_ + 256] == 0)
+    assert np.array_equal(ab, q.reshape(2, -1, 16).astype(np.int32).sum(axis=2).T.astype(np.int16))
+
+
+@pytest.mark.parametrize("qtype", [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_XS, F.IQ3_S])
+def test_blockdot_per256_vs_dequantized_double(qtype):
+    """blockdot256 (the act32 = false product) against float64 products of the dequantized weights and the
+    activations dequantized with their superblock scale."""
+    rng = np.random.default_rng(30 + qtype)
+    N, K, M = 40, 1024, 4
+    W = F.synth_weight(qtype, N, K, seed=200 + qtype)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
+    aq, asc, absum = oracle.quantize_act(x, act32=False)
+    C = oracle.blockdot256(qtype, W, K, aq, asc, absum)
+    w = oracle.dequant_rows(qtype, W, K).astype(np.float64)
+    xq = aq.astype(np.float64) * np.repeat(asc.T.astype(np.float64), 256, axis=1)
+    ref = xq @ w.T
+    assert np.max(np.abs(C - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
 def test_blockdot_column_sampling():
     W = F.synth_weight(F.IQ4_XS, 64, 512, seed=1)
     aq, asc, absum = oracle.quantize_act(np.random.default_rng(0).standard_normal((2, 512)).astype(np.float32))
