@@ -716,6 +716,140 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// MoE down projection, weight-stationary: a work-group owns 128 output columns (weight rows n of one expert, one
+// 32-row MFMA tile per wave) and walks `group` consecutive slot tiles of the tile list. Each lane decodes its row's
+// whole K = F (KB superblocks, 8 * KB 32-blocks of its k-half) into int8 MFMA B operands once per expert and keeps
+// them in registers (64 registers at F = 512), so an expert's weights are decoded once per work-group instead of once
+// per slot tile. Per slot tile: the 32 quantized h rows (int8, F bytes each), their per-32 scales and routing weights
+// are staged in LDS (the next tile's loads are issued before the current tile's MFMAs); per block pair two
+// v_mfma_i32_32x32x32_i8 give the exact int32 block sums, one 2-block f32 outer product asc * d * sc, and 32 VALU
+// scale-accumulate in f32 -- the arithmetic of gemm_kernel's MOE_DOWN mode, so the results are the same bits.
+// (Measured: double-buffered LDS with the y stores issued before the next tile's staging ran slower.)
+constexpr int RW_STRIDE = 16;  // LDS padding per staged row (bytes): rows of F + 16 bytes spread the operand reads
+
+template <int TYPE, int KB>
+__global__ __launch_bounds__(256, 2) void moe_down_rw_kernel(GemmArgs a, int group) {
+  constexpr int NB = 8 * KB, F = 256 * KB, RS = F + RW_STRIDE;
+  constexpr int ACH = 32 * F / 16 / 256;   // 16-byte chunks of the A tile per thread
+  constexpr int SCH = (NB * 32 + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint8_t sa[32 * RS];
+  __shared__ float ssc[NB * 32];
+  __shared__ float srs[32];
+  __shared__ typename LdsFor<TYPE>::type tab;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
+  const int ntile = a.tiles[0];
+  const int t0 = blockIdx.y * group;
+  if (t0 >= ntile) return;
+  const int t1 = min(t0 + group, ntile);
+  const int n_loc = blockIdx.x * 128 + wave * 32 + lc;  // output column = weight row within the expert
+  const bool col_ok = n_loc < a.expert_rows;
+  const uint32_t hfm = 0u - (uint32_t)hf;
+  lds_fill<TYPE>(&tab);
+  const KvTab kv = kv_tab();
+  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v32f zero32;
+#pragma unroll
+  for (int r = 0; r < 32; ++r) zero32[r] = 0.0f;
+
+  u32x4_t st_a[ACH];
+  float st_sc[SCH], st_rs = 0.0f;
+  auto fetch = [&](int t) {
+    const int m0 = a.tiles[2 + 3 * t], nr = a.tiles[3 + 3 * t];
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const int ch = tid + 256 * c, row = ch / (F / 16), col = ch % (F / 16);
+      st_a[c] = *(const u32x4_t*)(a.aq + (size_t)(m0 + min(row, nr - 1)) * F + col * 16);
+    }
+#pragma unroll
+    for (int c = 0; c < SCH; ++c) {
+      const int idx = min(tid + 256 * c, NB * 32 - 1), blk = idx >> 5, row = idx & 31;
+      st_sc[c] = a.asc[(size_t)blk * a.M_stride + m0 + min(row, nr - 1)];
+    }
+    if (tid < 32) st_rs = a.rowscale[m0 + min(tid, nr - 1)];
+  };
+
+  v4i bop[NB];
+  float my_dsc[NB / 2];
+  int cur_e = -1;
+  fetch(t0);
+  for (int t = t0; t < t1; ++t) {
+    const int e = a.tiles[1 + 3 * t], m0 = a.tiles[2 + 3 * t], nr = a.tiles[3 + 3 * t];
+    __syncthreads();  // (the previous tile's operand reads are done)
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const int ch = tid + 256 * c, row = ch / (F / 16), col = ch % (F / 16);
+      *(u32x4_t*)(sa + row * RS + col * 16) = st_a[c];
+    }
+#pragma unroll
+    for (int c = 0; c < SCH; ++c) {
+      const int idx = tid + 256 * c;
+      if (idx < NB * 32) ssc[idx] = st_sc[c];
+    }
+    if (tid < 32) srs[tid] = st_rs;
+    if (e != cur_e) {  // (uniform: one tile, one expert) this lane's row of expert e, decoded
+      cur_e = e;
+      const int n = e * a.expert_rows + min(n_loc, a.expert_rows - 1);
+#pragma unroll
+      for (int sb = 0; sb < KB; ++sb) {
+        uint4 pay[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) pay[b] = load_payload<TYPE>(a.w, n, sb * 8 + b, hf);
+        const uint4 hdr = load_header<TYPE>(a.w, n, sb);
+        float dsc[8], dmn[8];
+        int isc[8];
+        sb_scales<TYPE>(hdr, pay, dsc, dmn, isc);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) bop[sb * 8 + b] = b_operand<TYPE>(pay[b], hdr, b, hf, kv, &tab);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) my_dsc[sb * 4 + p] = lane_pick(hfm, dsc[2 * p], dsc[2 * p + 1]);
+      }
+    }
+    __syncthreads();
+    if (t + 1 < t1) fetch(t + 1);  // (the next tile's loads fly during this tile's MFMAs)
+    v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NB / 2; ++p) {
+      v16i dv[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint4 av = *(const uint4*)(sa + lc * RS + 32 * (2 * p + q) + 16 * hf);
+        const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+        dv[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[2 * p + q], zero16, 0, 0, 0);
+      }
+      const float my_asc = ssc[(2 * p + hf) * 32 + lc];
+      const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, my_dsc[p], zero32, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[r] = fmaf(sc[r], (float)dv[0][r], acc[r]);
+        acc[r] = fmaf(sc[16 + r], (float)dv[1][r], acc[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[r]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (i < nr && col_ok) a.C[(size_t)(m0 + i) * a.ldc + n_loc] = srs[i] * acc[r];
+    }
+  }
+}
+
+// Slot tiles per work-group of moe_down_rw_kernel
+// (measured at the BASELINE MoE shape: 2 tiles 257 us, 4 217, 8 207, 16 221)
+constexpr int kDownRwGroup = 8;
+
+template <int TYPE, int KB>
+static hipError_t go_down_rw(const GemmArgs& a, hipStream_t s) {
+  const unsigned gx = (unsigned)((a.expert_rows + 127) / 128);
+  const unsigned gy = (unsigned)((a.max_tiles + kDownRwGroup - 1) / kDownRwGroup);
+  moe_down_rw_kernel<TYPE, KB><<<dim3(gx, gy), dim3(256), 0, s>>>(a, kDownRwGroup);
+  return hipGetLastError();
+}
+
 template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go_s16(const GemmArgs& a, hipStream_t s) {
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
@@ -744,7 +878,13 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
     case GEMM_DENSE:
       return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
     case GEMM_MOE_GATEUP: return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
-    case GEMM_MOE_DOWN: return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
+    case GEMM_MOE_DOWN:
+      // (expert width F <= 512: the whole row's operands fit in registers; types with mins are not MoE types)
+      if constexpr (!Traits<TYPE>::MINS) {
+        if (a.w.K == 256) return go_down_rw<TYPE, 1>(a, s);
+        if (a.w.K == 512) return go_down_rw<TYPE, 2>(a, s);
+      }
+      return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
     case GEMM_MOE_G: return go<TYPE, 1, GEMM_MOE_G, false>(a, s);
     case GEMM_MOE_UH: return go<TYPE, 1, GEMM_MOE_UH, false>(a, s);
     default: return hipErrorInvalidValue;

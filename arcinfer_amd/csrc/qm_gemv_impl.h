@@ -115,11 +115,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
 // consecutive blocks read consecutive 16-byte words. DUMP: the same kernel writes each block's int32 sums
 // (dbg_isum, and Q4_K / Q5_K min sums to dbg_msum) instead of the output.
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP>
-__global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP, int NT = 256>
+__global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   extern __shared__ uint4 smem[];
   using Tr = Traits<TYPE>;
-  constexpr int GPW = 256 / LPR;                 // lane groups per work-group
+  constexpr int GPW = NT / LPR;                  // lane groups per work-group
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;   // waves per row
   const int K = a.w.K, nb = K / 32, rows = a.w.rows, T = a.T;
   // LDS: per token t < TB: int8 planes [2][nb][16] at t*K, then scales [TB][nb], then Q4_K block sums [TB][nb]
@@ -147,17 +147,51 @@ __global__ __launch_bounds__(256) void gemvs_kernel(GemvArgs a) {
   };
   fetch(0, cur);
   lds_fill<TYPE>(&lds);
-  for (int i = threadIdx.x; i < 2 * nb * TB; i += 256) {
-    const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
-    const int tt = min(t, T - 1);  // (tokens past T: a copy of the last, never stored)
-    *(uint4*)(sq + (size_t)t * K + (size_t)h * nb * 16 + b * 16) = *(const uint4*)(a.aq + (size_t)tt * K + 32 * b + 16 * h);
+  // staging: every thread issues all of its loads (at most SB 16-byte chunks, predicated) before its first LDS store
+  // (a loop of load -> store pairs waits out one L2 round trip per chunk)
+  constexpr int SB = 8;
+  for (int i0 = threadIdx.x; i0 < 2 * nb * TB; i0 += NT * SB) {
+    u32x4_t v[SB];  // (a native vector type: an array of uint4 structs would live in scratch memory)
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+      const int i = i0 + NT * k;
+      if (i < 2 * nb * TB) {
+        const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
+        const int tt = min(t, T - 1);  // (tokens past T: a copy of the last, never stored)
+        v[k] = *(const u32x4_t*)(a.aq + (size_t)tt * K + 32 * b + 16 * h);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+      const int i = i0 + NT * k;
+      if (i < 2 * nb * TB) {
+        const int t = i / (2 * nb), r = i % (2 * nb), b = r >> 1, h = r & 1;
+        *(u32x4_t*)(sq + (size_t)t * K + (size_t)h * nb * 16 + b * 16) = v[k];
+      }
+    }
   }
-  for (int i = threadIdx.x; i < nb * TB; i += 256) {
-    const int t = i / nb, b = i % nb, tt = min(t, T - 1);
-    if constexpr (!DUMP) ssc[i] = a.asc[(size_t)b * a.M_stride + tt];  // (the block-sum mode has no scales)
-    if constexpr (kNeedsBsum<TYPE>)
-      sbs[i] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride + tt] |
-               ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt] << 16);
+  for (int i0 = threadIdx.x; i0 < nb * TB; i0 += NT * SB) {
+    float sv[SB];
+    int bv[SB];
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+      const int i = i0 + NT * k;
+      if (i < nb * TB) {
+        const int t = i / nb, b = i % nb, tt = min(t, T - 1);
+        if constexpr (!DUMP) sv[k] = a.asc[(size_t)b * a.M_stride + tt];  // (the block-sum mode has no scales)
+        if constexpr (kNeedsBsum<TYPE>)
+          bv[k] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride + tt] |
+                  ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride + tt] << 16);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+      const int i = i0 + NT * k;
+      if (i < nb * TB) {
+        if constexpr (!DUMP) ssc[i] = sv[k];
+        if constexpr (kNeedsBsum<TYPE>) sbs[i] = bv[k];
+      }
+    }
   }
   __syncthreads();
   const KvTab kv = kv_tab();
