@@ -127,7 +127,8 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   float* ssc = (float*)(sq + (size_t)TB * K);
   int* sbs = (int*)(ssc + (size_t)TB * nb);
   __shared__ typename LdsFor<TYPE>::type lds;
-  __shared__ float part[2][GPW][WPR][TB];
+  constexpr int RC = WPR > 1 ? 8 : 1;  // rows per cross-wave combine (several waves per row)
+  __shared__ float part[2][RC][GPW][WPR][TB];
   const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
   const int G = gridDim.x * GPW;
   const int g0 = blockIdx.x * GPW + grp;
@@ -227,25 +228,39 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
         }
       }
     }
-    const int n = g0 + G * i;
-    float v[TB];
-    if constexpr (WPR == 1) {
-#pragma unroll
-      for (int t = 0; t < TB; ++t) v[t] = wave_sum_width(acc[t], LPR);
-    } else {
+    if constexpr (WPR > 1) {
+      // each wave's row sum goes to LDS; every RC rows one barrier, then lane j of the group adds the WPR partials of
+      // the chunk's row j (in wave order) and stores it. Two chunk buffers: a chunk's partials are read after the
+      // barrier that ends it and overwritten only after the next one.
+      const int hb = (i / RC) & 1, slot = i % RC;
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
         const float w = wave_sum_width(acc[t], 64);
-        if ((threadIdx.x & 63) == 0) part[i & 1][grp][gl >> 6][t] = w;
+        if ((threadIdx.x & 63) == 0) part[hb][slot][grp][gl >> 6][t] = w;
       }
-      __syncthreads();  // (double-buffered by step parity: one barrier per step)
+      if (slot == RC - 1 || i == steps - 1) {
+        __syncthreads();
+        const int nj = slot + 1, j = gl;
+        const int nr = g0 + G * (i - slot + j);
+        if (!DUMP && j < nj && nr < rows) {
 #pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        v[t] = part[i & 1][grp][0][t];
+          for (int t = 0; t < TB; ++t) {
+            float v = part[hb][j][grp][0][t];
 #pragma unroll
-        for (int k = 1; k < WPR; ++k) v[t] += part[i & 1][grp][k][t];
+            for (int k = 1; k < WPR; ++k) v += part[hb][j][grp][k][t];
+            if (t < T) {
+              float* cp = a.C + (size_t)t * a.ldc + a.c_off + nr;
+              *cp = a.accumulate ? *cp + v : v;
+            }
+          }
+        }
       }
+      return;
     }
+    const int n = g0 + G * i;
+    float v[TB];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) v[t] = wave_sum_width(acc[t], LPR);
     if (!DUMP && gl == 0 && n < rows) {
 #pragma unroll
       for (int t = 0; t < TB; ++t)
