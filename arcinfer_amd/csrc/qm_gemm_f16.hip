@@ -127,18 +127,23 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t c
 
 // Q4_K: the lane's 16 values of one 32-block (payload bytes 8h..8h+7: x, y) times the integer block scale, as two
 // f16 operands: chunk 0 the low nibbles (elements 8h + perm8(i)), chunk 1 the high nibbles (16 + 8h + perm8(i)).
-// (1024 + q) as f16 is the bit pattern 0x6400 | q; one packed fma makes (1024 + q) sc - 1024 sc = sc q exactly.
+// (1024 + q) as f16 is the bit pattern 0x6400 | q; one packed fma makes (1024 + q) sc - 1024 sc = sc q exactly. The
+// high nibbles are not shifted down: left in mantissa bits 4-7 under the exponent of 16384 (0x7400 | q << 4) they
+// read as 16384 + 256 q, and (16384 + 256 q) (sc / 256) - 64 sc = sc q exactly too (sc / 256 and 64 sc are exact in
+// f16, and the fused multiply-add rounds only its exact integer result).
 __device__ __forceinline__ void q4k_f16_decode(uint32_t x, uint32_t y, int sc, uint32_t c64, f16x8& b0, f16x8& b1) {
   const _Float16 s = (_Float16)sc;
   const f16x2 sc2 = {s, s}, off2 = {(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
-  const uint32_t m = 0x000F000Fu;
-  const uint32_t w[8] = {and_or(x, m, c64), and_or(x >> 8, m, c64), and_or(y, m, c64), and_or(y >> 8, m, c64),
-                         and_or(x >> 4, m, c64), and_or(x >> 12, m, c64), and_or(y >> 4, m, c64),
-                         and_or(y >> 12, m, c64)};
+  const _Float16 sh = s * (_Float16)0.00390625f;  // sc / 256
+  const f16x2 sch2 = {sh, sh}, offh2 = {(_Float16)(-64.0f) * s, (_Float16)(-64.0f) * s};
+  const uint32_t m = 0x000F000Fu, mh = 0x00F000F0u, c74 = 0x74007400u;
+  const uint32_t x8 = x >> 8, y8 = y >> 8;
+  const uint32_t w[8] = {and_or(x, m, c64), and_or(x8, m, c64), and_or(y, m, c64), and_or(y8, m, c64),
+                         and_or(x, mh, c74), and_or(x8, mh, c74), and_or(y, mh, c74), and_or(y8, mh, c74)};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const f16x2 v0 = __builtin_bit_cast(f16x2, w[i]) * sc2 + off2;
-    const f16x2 v1 = __builtin_bit_cast(f16x2, w[4 + i]) * sc2 + off2;
+    const f16x2 v1 = __builtin_bit_cast(f16x2, w[4 + i]) * sch2 + offh2;
     b0[2 * i] = v0[0];
     b0[2 * i + 1] = v0[1];
     b1[2 * i] = v1[0];
@@ -161,6 +166,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   // two activation stages of 16 KB, reused at the end to transpose the result tiles (4 waves x 32 x 33 floats)
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kF16PairBytes];
   __shared__ float dtab[4][2][32];  // per wave: d and dmin of its 32 rows (current superblock)
+  __shared__ float sasc[2][2][kF16BM];  // per stage: the activation scales of the pair's two blocks, [block][token]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, lc = lane & 31;
   const int K = a.w.K, nb = K / 32, nsb = K / 256, npair = K / 64;
   int nt, mt;
@@ -173,8 +179,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   const uint8_t* hrow = a.w.hdr + (size_t)nrow * nsb * 16;
   const uint8_t* abase = a.af + (size_t)mt * npair * kF16PairBytes;
   const uint32_t c64 = 0x64006400u;
-  const int mrow[4] = {min(m0 + lc, a.M - 1), min(m0 + 32 + lc, a.M - 1), min(m0 + 64 + lc, a.M - 1),
-                       min(m0 + 96 + lc, a.M - 1)};
 
   // activation staging: 16 KB per block pair, 4 x 16 bytes per thread
   u32x4_t st[4];
@@ -186,13 +190,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) *(u32x4_t*)(lds + buf * kF16PairBytes + (tid + 256 * c) * 16) = st[c];
   };
-  // activation scales of a block pair: asc[blk][token], one per lane and token tile
-  float sa[2][4], sa_n[2][4];
-  auto load_sa = [&](int g, float (&v)[2][4]) {
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[bb][t] = a.asc[(size_t)((2 * g + bb) >> a.ash) * a.M_stride + mrow[t]];
+  // activation scales of a block pair, staged with its activations: thread tid takes block tid / 128, token tid % 128
+  float st_sc;
+  const int sc_row = min(m0 + (tid & (kF16BM - 1)), a.M - 1);
+  // (the block-sum mode has no activation scales: a.asc is null there and is never read)
+  auto fetch_sa = [&](int g) {
+    if constexpr (!DUMP) st_sc = a.asc[(size_t)((2 * g + (tid >> 7)) >> a.ash) * a.M_stride + sc_row];
+  };
+  auto store_sa = [&](int buf) {
+    if constexpr (!DUMP) sasc[buf][tid >> 7][tid & (kF16BM - 1)] = st_sc;
   };
 
   f32x16 tq[4], res[4];
@@ -206,9 +212,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   uint2 pay[2], pay_n[2];
 #pragma unroll
   for (int bb = 0; bb < 2; ++bb) pay[bb] = *(const uint2*)(qrow + bb * 16);
-  load_sa(0, sa);
+  fetch_sa(0);
   fetch(0);
   store(0);
+  store_sa(0);
   __syncthreads();
 
   for (int s = 0; s < nsb; ++s) {
@@ -221,7 +228,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
       fetch(gn);
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) pay_n[bb] = *(const uint2*)(qrow + (size_t)(2 * gn + bb) * 16);
-      load_sa(gn, sa_n);
+      fetch_sa(gn);
       // (keeps the loads here: issued a whole pair of MFMA work before their data is needed)
       __builtin_amdgcn_sched_barrier(0);
       f16x8 aw[2][2];
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
               if (m < a.M && n < n_rows) a.dbg_isum[((size_t)m * n_rows + n) * nb + blk] = (int)Iprev[r];
             }
           } else {
-            const float sv = sa[bb][t];
+            const float sv = sasc[cur][bb][32 * t + lc];
 #pragma unroll
             for (int r = 0; r < 16; ++r)
               tq[t][r] = (p == 0 && bb == 0) ? sv * Iprev[r] : fmaf(sv, Iprev[r], tq[t][r]);
@@ -272,12 +279,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
       }
       __builtin_amdgcn_sched_barrier(0);
       store(cur ^ 1);
+      store_sa(cur ^ 1);
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) pay[bb] = pay_n[bb];
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) sa[bb][t] = sa_n[bb][t];
       __syncthreads();
     }
     if constexpr (!DUMP) {
