@@ -161,7 +161,11 @@ __device__ __forceinline__ void f16_tile(int& nt, int& mt) {
   nt = lin % gx;
 }
 
-template <int TYPE, bool DUMP>
+// S256: per-256 activation scales (the reference's act32 = false, gemm.cl:413-447): one scale per token and superblock,
+// so the f16 MFMAs accumulate the whole superblock's products (sum_b sc * isum, in f32: exact while the partial sums
+// stay below 2^24, i.e. for all but extreme rows, and within f32 rounding otherwise) and the scale is applied once per
+// superblock, res = fma(d * asc, I, fma(-dmin, tmn, res)) -- no per-block VALU work.
+template <int TYPE, bool DUMP, bool S256 = false>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   // two activation stages of 16 KB, reused at the end to transpose the result tiles (4 waves x 32 x 33 floats)
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kF16PairBytes];
@@ -240,42 +244,56 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         q4k_f16_decode(pay[bb].x, pay[bb].y, sc, c64, aw[bb][0], aw[bb][1]);
       }
       const uint8_t* L = lds + cur * kF16PairBytes + lane * 16;
-      // items k = (token tile t, block bb), t = k / 2, bb = k % 2: stage k issues item k's two MFMAs and scales item
-      // k - 1's block sums, so one MFMA result is in flight while the previous one is consumed
-      f32x16 Iprev;
+      if constexpr (S256) {
+        // items block-major (k = 4 bb + t): consecutive MFMAs feed different token tiles' accumulators
 #pragma unroll
-      for (int k = 0; k <= 8; ++k) {
-        f32x16 Icur;
-        if (k < 8) {
-          const int t = k >> 1, bb = k & 1;
+        for (int k = 0; k < 8; ++k) {
+          const int t = k & 3, bb = k >> 2;
           const uint8_t* Lt = L + t * kF16PairTile;
           const f16x8 b0 = *(const f16x8*)(Lt + (2 * bb) * kF16Piece);
           const f16x8 b1 = *(const f16x8*)(Lt + (2 * bb + 1) * kF16Piece);
-          Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][0], b0, zero16, 0, 0, 0);
-          Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, Icur, 0, 0, 0);
+          const f32x16 c = (p == 0 && bb == 0) ? zero16 : tq[t];
+          tq[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][0], b0, c, 0, 0, 0);
+          tq[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, tq[t], 0, 0, 0);
         }
-        if (k > 0) {
-          const int t = (k - 1) >> 1, bb = (k - 1) & 1;
-          if constexpr (DUMP) {
-            const int m = m0 + 32 * t + lc, blk = 8 * s + 2 * p + bb;
+      } else {
+        // items k = (token tile t, block bb), t = k / 2, bb = k % 2: stage k issues item k's two MFMAs and scales
+        // item k - 1's block sums, so one MFMA result is in flight while the previous one is consumed
+        f32x16 Iprev;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int n = nbase + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (m < a.M && n < n_rows) a.dbg_isum[((size_t)m * n_rows + n) * nb + blk] = (int)Iprev[r];
-            }
-          } else {
-            const float sv = sasc[cur][bb][32 * t + lc];
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              tq[t][r] = (p == 0 && bb == 0) ? sv * Iprev[r] : fmaf(sv, Iprev[r], tq[t][r]);
-            // (pins the scaled sums here: otherwise the compiler defers every fma to the superblock end and keeps
-            // each block's MFMA result alive meanwhile, in scratch memory)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(tq[t][r]));
+        for (int k = 0; k <= 8; ++k) {
+          f32x16 Icur;
+          if (k < 8) {
+            const int t = k >> 1, bb = k & 1;
+            const uint8_t* Lt = L + t * kF16PairTile;
+            const f16x8 b0 = *(const f16x8*)(Lt + (2 * bb) * kF16Piece);
+            const f16x8 b1 = *(const f16x8*)(Lt + (2 * bb + 1) * kF16Piece);
+            Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][0], b0, zero16, 0, 0, 0);
+            Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, Icur, 0, 0, 0);
           }
+          if (k > 0) {
+            const int t = (k - 1) >> 1, bb = (k - 1) & 1;
+            if constexpr (DUMP) {
+              const int m = m0 + 32 * t + lc, blk = 8 * s + 2 * p + bb;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int n = nbase + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < a.M && n < n_rows) a.dbg_isum[((size_t)m * n_rows + n) * nb + blk] = (int)Iprev[r];
+              }
+            } else {
+              const float sv = sasc[cur][bb][32 * t + lc];
+#pragma unroll
+              for (int r = 0; r < 16; ++r)
+                tq[t][r] = (p == 0 && bb == 0) ? sv * Iprev[r] : fmaf(sv, Iprev[r], tq[t][r]);
+              // (pins the scaled sums here: otherwise the compiler defers every fma to the superblock end and keeps
+              // each block's MFMA result alive meanwhile, in scratch memory)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(tq[t][r]));
+            }
+          }
+          if (k < 8) Iprev = Icur;
+          __builtin_amdgcn_sched_barrier(0);
         }
-        if (k < 8) Iprev = Icur;
-        __builtin_amdgcn_sched_barrier(0);
       }
       __builtin_amdgcn_sched_barrier(0);
       store(cur ^ 1);
@@ -315,8 +333,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
       for (int t = 0; t < 4; ++t) {
         const uint4 uv = *(const uint4*)(a.u + (size_t)(m0 + 32 * t + lc) * nb + 8 * s + 4 * h);
         const f32x16 tmn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mnop, __builtin_bit_cast(bf16x8, uv), zero16, 0, 0, 0);
+        if constexpr (S256) {
+          const float sv = sasc[(4 * s + 3) & 1][0][32 * t + lc];  // (the superblock's scale: its last pair's stage)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) res[t][r] = fmaf(dr[r], tq[t][r], fmaf(dmr[r], tmn[r], res[t][r]));
+          for (int r = 0; r < 16; ++r) res[t][r] = fmaf(dr[r] * sv, tq[t][r], fmaf(dmr[r], tmn[r], res[t][r]));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) res[t][r] = fmaf(dr[r], tq[t][r], fmaf(dmr[r], tmn[r], res[t][r]));
+        }
       }
     }
     hdr = hdr_n;
@@ -449,6 +473,7 @@ hipError_t launch_gemm_f16(int type, const GemmArgs& g, void* ws, hipStream_t s)
     a.dbg_isum = g.dbg_isum;
     const dim3 grid((unsigned)((g.w.rows + kF16BN - 1) / kF16BN), (unsigned)(Mp / kF16BM));
     if (g.dbg_isum) gemm_f16_kernel<T_Q4_K, true><<<grid, dim3(256), 0, s>>>(a);
+    else if (g.ash == 3) gemm_f16_kernel<T_Q4_K, false, true><<<grid, dim3(256), 0, s>>>(a);
     else gemm_f16_kernel<T_Q4_K, false><<<grid, dim3(256), 0, s>>>(a);
     e = hipGetLastError();
   }

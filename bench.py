@@ -254,6 +254,14 @@ def main():
                 "matmul_f32": {"value": round(2.0 * Ms_ * N * K / f_s / 1e12, 5), "unit": "TFLOP/s", "cores": nthreads,
                                "kind": "port",
                                "sample": f"the first {Ms_} tokens of the same GEMM, f32 dequantized weights, f64 dots"}}
+        # the same Q4_K GEMM with per-256 activation scales (the reference's act32 = false layout, qmatmul_gemm_ex):
+        # one scale per token and superblock, so the f16 MFMAs accumulate the superblock and no per-block VALU scaling
+        # runs (reported beside the per-32 headline; the inputs are this x quantized per 256)
+        aq2, asc2, absum2 = qm.quantize_act(x, act32=False)
+        ms2, _ = timed(lambda i: qm.gemm(w, aq2, asc2, absum2, C=C, ldc=N, act32=False), steps, args.warmup, stream)
+        g["act32_false"] = {"TOPS": round(ops / (ms2 * 1e-3) / 1e12, 1), "ms_per_launch": round(ms2, 4),
+                            "frac_of_int8_peak": round(ops / (ms2 * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        del aq2, asc2, absum2
         # the same prompt GEMM with Q6_K weights (per-16 scales: two K=16 MFMAs per block), reported
         W6 = F.synth_weight(F.Q6_K, N, K, seed=6)
         w6 = qm.QWeight(F.Q6_K, torch.from_numpy(W6).to(dev), N, K)
