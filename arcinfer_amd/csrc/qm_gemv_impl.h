@@ -227,6 +227,9 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
           }
         }
       }
+      // (eight tokens: one block's token rows at a time -- left free, the compiler reads every block's rows for
+      // every token from LDS up front and runs out of registers)
+      if constexpr (TB >= 8) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (WPR > 1) {
       // each wave's row sum goes to LDS; every RC rows one barrier, then lane j of the group adds the WPR partials of
