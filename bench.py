@@ -32,7 +32,9 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    # (2000 warm-up steps, ~50 ms of GEMV work: the GPU's clocks settle under load within tens of milliseconds; with 20
+    #  the timed steps ran ~15 % slower while the clocks were still rising)
+    p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--only", choices=["all", "gemv", "gemm", "moe", "report"], default="all")
     p.add_argument("--copies", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
