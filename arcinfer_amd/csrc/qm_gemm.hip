@@ -260,6 +260,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   __shared__ GemmLds<TYPE, MT> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lc = lane & 31;
   const int K = a.w.K, nb = K / 32, nsb = K / 256;
+  // K split (dense, gridDim.z = 2): this work-group's superblocks [sb0, sb1); the two halves are added into a zeroed C
+  const int sb0 = (int)blockIdx.z * nsb / (int)gridDim.z, sb1 = ((int)blockIdx.z + 1) * nsb / (int)gridDim.z;
 
   // ---- which rows: dense (M tile), or one MoE tile (expert e, slots r0 .. r0 + nr - 1)
   int m0, nvalid, wrow0, nt;
@@ -322,12 +324,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   uint4 pay[8], pay2[GU ? 8 : 1];
   uint4 hdr, hdr2 = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) pay[b] = load_payload<TYPE>(a.w, n, b, hf);
-  hdr = load_header<TYPE>(a.w, n, 0);
+  for (int b = 0; b < 8; ++b) pay[b] = load_payload<TYPE>(a.w, n, sb0 * 8 + b, hf);
+  hdr = load_header<TYPE>(a.w, n, sb0);
   if constexpr (GU) {
 #pragma unroll
-    for (int b = 0; b < 8; ++b) pay2[b] = load_payload<TYPE>(a.w2, n, b, hf);
-    hdr2 = load_header<TYPE>(a.w2, n, 0);
+    for (int b = 0; b < 8; ++b) pay2[b] = load_payload<TYPE>(a.w2, n, sb0 * 8 + b, hf);
+    hdr2 = load_header<TYPE>(a.w2, n, sb0);
   }
 
   v16f acc[MT], acc2[GU ? MT : 1];
@@ -345,13 +347,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int r = 0; r < 32; ++r) zero32[r] = 0.0f;
 
-  QM_FETCH_ACTS(0)
+  QM_FETCH_ACTS(sb0)
   QM_STORE_ACTS(0)
   __syncthreads();
 
-  for (int s = 0; s < nsb; ++s) {
-    const int cur = s & 1;
-    const int sn = s + 1 < nsb ? s + 1 : s;  // (the last superblock reloads itself: no conditional register state)
+  for (int s = sb0; s < sb1; ++s) {
+    const int cur = (s - sb0) & 1;
+    const int sn = s + 1 < sb1 ? s + 1 : s;  // (the last superblock reloads itself: no conditional register state)
     QM_FETCH_ACTS(sn)
 
     float dsc[8], dmn[8], dsc2[8], dmn2[8];
@@ -510,6 +512,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         if (row_ok && col_ok) {
           float* cp = a.C + (size_t)(m0 + i) * a.ldc + a.c_off + n_loc;
           float v = acc[mt][r];
+          if (gridDim.z > 1) {  // (K split: C was zeroed; 0 + x + y is the same float in either order)
+            unsafeAtomicAdd(cp, v);
+            continue;
+          }
           if (a.accumulate == 1) {
             v += *cp;
           } else if (a.accumulate == 2) {
@@ -860,13 +866,28 @@ static hipError_t go_s16(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// zeroes C[m][c_off .. c_off + n) for m < M (a kernel, not a memset, so the call stays capturable in a HIP graph)
+__global__ void zero_rows_kernel(float* C, int ldc, int c_off, int n, int M) {
+  const int m = blockIdx.y;
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) C[(size_t)m * ldc + c_off + j] = 0.0f;
+}
+
 template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go(const GemmArgs& a, hipStream_t s) {
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
   const unsigned gx = (unsigned)((n_rows + 127) / 128);
   const unsigned gy = MODE == GEMM_DENSE ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT))
                                           : (unsigned)(a.max_tiles * (kMoeTileRows / (32 * MT)));
-  gemm_kernel<TYPE, MT, MODE, DUMP><<<dim3(gx, gy), dim3(256), 0, s>>>(a);
+  // A dense product with too few tiles to give every CU two work-groups (M = 512, N = 5120: 320 tiles) splits K in two:
+  // each half adds its partial sums into a zeroed C, so the grid doubles. Two partials keep the result deterministic
+  // (0 + x + y rounds the same in either order); only with accumulate = 0 (C + x + y would not).
+  unsigned gz = 1;
+  if (MODE == GEMM_DENSE && !DUMP && a.accumulate == 0 && gx * gy < 512 && a.w.K / 256 >= 8) {
+    gz = 2;
+    zero_rows_kernel<<<dim3((unsigned)((n_rows + 255) / 256), (unsigned)a.M), dim3(256), 0, s>>>(a.C, a.ldc, a.c_off,
+                                                                                                   n_rows, a.M);
+  }
+  gemm_kernel<TYPE, MT, MODE, DUMP><<<dim3(gx, gy, gz), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }
 

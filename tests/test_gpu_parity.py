@@ -311,3 +311,28 @@ def test_gemm_q4_k_edges(qm, dev, M, N, K, c_off, extra):
     assert rel_err(Cn[:, c_off:c_off + N], ref) < TOL_INT8_PATH
     assert np.all(Cn[:, :c_off] == 7.0) and np.all(Cn[:, c_off + N:] == 7.0)
     assert np.all(Cn[:, c_off + 2] == 0.0)  # row 2 of the weight is all zero
+
+
+def test_gemm_k_split_is_deterministic_and_stays_in_its_columns(qm, dev):
+    """A dense product with few tiles splits K in two (the halves are added into C after it is zeroed): the result is
+    the same bits on every call, the columns outside [c_off, c_off + N) are untouched, and it meets the f32 bars."""
+    import torch
+    M, N, K = 100, 384, 2048
+    W = F.synth_weight(F.IQ3_S, N, K, seed=17)
+    x = F.synth_activations(M, K, seed=18)
+    aq, asc, absum = acts(qm, x, dev)
+    w = qm.QWeight(F.IQ3_S, to_dev(W, dev), N, K)
+    ldc = N + 40
+    C = torch.full((M, ldc), float("nan"), device=dev)
+    qm.gemm(w, aq, asc, absum, C=C, ldc=ldc, c_off=24)
+    first = C.clone()
+    for _ in range(3):
+        C.fill_(float("nan"))
+        qm.gemm(w, aq, asc, absum, C=C, ldc=ldc, c_off=24)
+        torch.cuda.synchronize()
+        assert torch.equal(C[:, 24:24 + N], first[:, 24:24 + N])
+    assert torch.all(torch.isnan(C[:, :24])) and torch.all(torch.isnan(C[:, 24 + N:]))
+    ref = oracle.blockdot(F.IQ3_S, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy())
+    got = first[:, 24:24 + N].cpu().numpy()
+    assert rel_err(got, ref) < TOL_INT8_PATH
+    assert_elementwise(got, ref)
