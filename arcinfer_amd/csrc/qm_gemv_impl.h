@@ -115,8 +115,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
 // consecutive blocks read consecutive 16-byte words. DUMP: the same kernel writes each block's int32 sums
 // (dbg_isum, and Q4_K / Q5_K min sums to dbg_msum) instead of the output.
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP, int NT = 256>
+//
+// AREG (batch 1 only): lane j reads the same blocks of the token row for every weight row, so it loads them once into
+// registers (two 16-byte words, the scale and the Q4_K / Q5_K / Q6_K sums per block) and nothing is staged in LDS.
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP, bool AREG = false, int NT = 256>
 __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
+  static_assert(!AREG || TB == 1, "token blocks in registers: batch 1 only");
   extern __shared__ uint4 smem[];
   using Tr = Traits<TYPE>;
   constexpr int GPW = NT / LPR;                  // lane groups per work-group
@@ -148,9 +152,24 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   };
   fetch(0, cur);
   lds_fill<TYPE>(&lds);
+  u32x4_t xr[AREG ? CH : 1][2];
+  float xs[AREG ? CH : 1];
+  int xb[AREG ? CH : 1];
+  if constexpr (AREG) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int b = EXACT ? gl + LPR * u : min(gl + LPR * u, nb - 1);
+      xr[u][0] = *(const u32x4_t*)(a.aq + 32 * b);
+      xr[u][1] = *(const u32x4_t*)(a.aq + 32 * b + 16);
+      if constexpr (!DUMP) xs[u] = a.asc[(size_t)b * a.M_stride];
+      if constexpr (kNeedsBsum<TYPE>)
+        xb[u] = (int)(uint16_t)a.absum[(size_t)(2 * b) * a.M_stride] | ((int)a.absum[(size_t)(2 * b + 1) * a.M_stride] << 16);
+    }
+  }
   // staging: every thread issues all of its loads (at most SB 16-byte chunks, predicated) before its first LDS store
   // (a loop of load -> store pairs waits out one L2 round trip per chunk)
   constexpr int SB = 8;
+  if constexpr (!AREG)
   for (int i0 = threadIdx.x; i0 < 2 * nb * TB; i0 += NT * SB) {
     u32x4_t v[SB];  // (a native vector type: an array of uint4 structs would live in scratch memory)
 #pragma unroll
@@ -171,6 +190,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
       }
     }
   }
+  if constexpr (!AREG)
   for (int i0 = threadIdx.x; i0 < nb * TB; i0 += NT * SB) {
     float sv[SB];
     int bv[SB];
@@ -211,9 +231,18 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
         decode_block32<TYPE>(cur[u], &lds, b & 7, kv, wd, sc, sc1, mn, bi.d, bi.dmin);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
-          const uint8_t* st = sq + (size_t)t * K;
-          const uint4 x0 = *(const uint4*)(st + b * 16), x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
-          const int bp = kNeedsBsum<TYPE> ? sbs[t * nb + b] : 0;
+          uint4 x0, x1;
+          int bp;
+          if constexpr (AREG) {
+            x0 = uint4{xr[u][0][0], xr[u][0][1], xr[u][0][2], xr[u][0][3]};
+            x1 = uint4{xr[u][1][0], xr[u][1][1], xr[u][1][2], xr[u][1][3]};
+            bp = kNeedsBsum<TYPE> ? xb[u] : 0;
+          } else {
+            const uint8_t* st = sq + (size_t)t * K;
+            x0 = *(const uint4*)(st + b * 16);
+            x1 = *(const uint4*)(st + (size_t)nb * 16 + b * 16);
+            bp = kNeedsBsum<TYPE> ? sbs[t * nb + b] : 0;
+          }
           block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16, bi.iv, bi.mv);
           if constexpr (DUMP) {
             const int n = g0 + G * i;
@@ -223,7 +252,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
               if constexpr (Traits<TYPE>::MINS) a.dbg_msum[o] = bi.mv;
             }
           } else {
-            acc[t] += block_value<TYPE>(ssc[t * nb + b], bi);
+            acc[t] += block_value<TYPE>(AREG ? xs[u] : ssc[t * nb + b], bi);
           }
         }
       }
@@ -304,21 +333,21 @@ static size_t gemvs_lds(int type, int K, int TB) {
   return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
 }
 
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP>
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = false, int PC = (LPR == 256 ? 3 : 2)>
 static hipError_t gos(const GemvArgs& a, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
   constexpr int PF = TB == 1 ? 2 : 1;  // batch 1: two rows in flight per lane group; more tokens: registers to tokens
-  // Persistent grid: two work-groups per CU (three with four waves per row), or as many as the kernel's registers and
-  // LDS let reside (the 8-token instantiation needs more than 256 registers: one wave per SIMD), so the whole grid is
-  // resident at once; fewer when the matrix has fewer rows than lane groups. Occupancy is queried once, for this
-  // instantiation's largest K.
+  // Persistent grid: PC work-groups per CU (two; three with four waves per row or where measured faster), or as many
+  // as the kernel's registers and LDS let reside (the 8-token instantiation needs more than 256 registers: one wave per
+  // SIMD), so the whole grid is resident at once; fewer when the matrix has fewer rows than lane groups. Occupancy is
+  // queried once, for this instantiation's largest K.
   static const int per_cu = [] {
     int n = 0;
-    const size_t lds_max = gemvs_lds(TYPE, 32 * LPR * CH, TB);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false>, 256, lds_max) !=
+    const size_t lds_max = AREG ? 0 : gemvs_lds(TYPE, 32 * LPR * CH, TB);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false, AREG>, 256, lds_max) !=
             hipSuccess || n < 1)
       n = 1;
-    return min(LPR == 256 ? 3 : 2, n);
+    return min(PC, n);
   }();
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -328,7 +357,7 @@ static hipError_t gos(const GemvArgs& a, hipStream_t s) {
     return n;
   }();
   const int wgs = min(per_cu * cus, (a.w.rows + GPW - 1) / GPW);
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP><<<wgs, 256, gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG><<<wgs, 256, AREG ? 0 : gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
 
@@ -379,7 +408,16 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
         if (a.dbg_msum) c.dbg_msum = a.dbg_msum + (size_t)t0 * a.w.rows * nb;
       }
       hipError_t e;
-      if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
+      if (a.T == 1 && nb <= 256 && a.w.rows <= 6144) {
+        // batch 1, a small matrix (the grid has about one row per 32-lane group): 128 lanes per row, token blocks in
+        // registers, three work-groups per CU. Measured against 32 lanes per row: Q8_0 4096 x 4096 6.8 -> 6.4 us,
+        // IQ3_S 5120 x 5120 7.7 -> 6.8 us, IQ4_XS 5120 x 5120 6.7 -> 6.2 us
+        e = nb <= 128 ? gos<TYPE, 128, 1, false, 1, DUMP, true, 3>(c, s) : gos<TYPE, 128, 2, false, 1, DUMP, true, 3>(c, s);
+      } else if (a.T == 1 && nb > 512 && nb <= 768) {
+        // batch 1, long rows: 128 lanes (two waves) per row, token blocks in registers: the 17408-wide down projection
+        // (544 blocks) at 11.9 us against 12.3 us with four waves per row and the token row in LDS
+        e = nb <= 640 ? gos<TYPE, 128, 5, false, 1, DUMP, true>(c, s) : gos<TYPE, 128, 6, false, 1, DUMP, true>(c, s);
+      } else if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
         switch ((nb + 31) / 32) {
           case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true, DUMP>(c, s) : gos_tb<TYPE, 32, 1, false, DUMP>(c, s); break;
           case 2: e = nb == 64 ? gos_tb<TYPE, 32, 2, true, DUMP>(c, s) : gos_tb<TYPE, 32, 2, false, DUMP>(c, s); break;
@@ -391,8 +429,7 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
           default: e = nb == 256 ? gos_tb<TYPE, 32, 8, true, DUMP>(c, s) : gos_tb<TYPE, 32, 8, false, DUMP>(c, s); break;
         }
       } else if (nb > 512 && nb <= 768) {
-        // 256 lanes (the work-group's four waves) per row, 3 blocks per lane, three work-groups per CU: measured on
-        // the 17408-wide down projection (544 blocks) at 13.8 us against 14.8 us with two waves per row
+        // several tokens: 256 lanes (the work-group's four waves) per row, 3 blocks per lane, three work-groups per CU
         e = nb == 768 ? gos_tb<TYPE, 256, 3, true, DUMP>(c, s) : gos_tb<TYPE, 256, 3, false, DUMP>(c, s);
       } else {  // long rows: 128 lanes (two waves) per row, up to 8 blocks per lane
         switch ((nb + 127) / 128) {

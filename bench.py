@@ -174,7 +174,7 @@ def main():
         dom_key = max(per, key=lambda k: per[k]["us_per_launch"])
         dom = per[dom_key]
         Kd, Nd = (int(v) for v in dom_key.split("->"))
-        lpr = 256 if 512 < Kd // 32 <= 768 else (32 if Kd // 32 <= 256 else 128)
+        lpr = 32 if Kd // 32 <= 256 and Nd > 6144 else 128  # (the batch-1 route of qm_gemv_impl.h)
         traffic = profile_traffic(f"gemv_iq4_xs_{Kd}x{Nd}")
         out["roofline"] = {"bound": "hbm",
                            "kernel": f"gemvs_kernel (IQ4_XS, {lpr} lanes per row) K={Kd} N={Nd}: the step's longer launch",
