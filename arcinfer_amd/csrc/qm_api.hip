@@ -98,7 +98,7 @@ int ensure_init() {
   } while (0)
 
 struct MoeLayout {
-  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, hf, total;
+  size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, hf, part, total;
   int slots, max_tiles, tile_rows;
 };
 
@@ -127,6 +127,7 @@ MoeLayout moe_layout(int T, int NE, int NU, int E, int F) {
   L.hsc = take(sizeof(float) * (size_t)(F / 32) * L.slots);
   L.y = take(sizeof(float) * (size_t)L.slots * E);
   L.hf = take(sizeof(float) * (size_t)L.slots * F);
+  L.part = take(sizeof(int) * (size_t)qm::moe_route_groups(T) * NE);  // routing histograms, then running sums
   L.total = o;
   return L;
 }
@@ -493,7 +494,7 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = hipSuccess;
   if (counts) e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
-  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, nullptr, s);
+  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, nullptr, nullptr, s);
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_route");
 }
 
@@ -550,10 +551,11 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
                                                accumulate, shd, s);
     return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
   }
-  hipError_t e = qm::launch_fill_i32(counts, 0, (size_t)NE, s);
-  if (e == hipSuccess) e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, counts, escale, s);
-  if (e == hipSuccess) e = qm::launch_moe_scan(counts, cursor, tstart, tiles, NE, L.tile_rows, s);
-  if (e == hipSuccess) e = qm::launch_moe_scatter(ids, wts, L.slots, NU, NE, cursor, stok, swt, inv, s);
+  int* part = (int*)(b + L.part);
+  hipError_t e = qm::launch_moe_route(logits, ldl, T, NE, NU, ids, wts, nullptr, escale, part, s);
+  if (e == hipSuccess) e = qm::launch_moe_scan(part, qm::moe_route_groups(T), counts, NE, s);
+  if (e == hipSuccess)
+    e = qm::launch_moe_scatter(ids, wts, T, NU, NE, part, counts, cursor, tstart, tiles, L.tile_rows, stok, swt, inv, s);
   // gate and up: one launch when they share a type the int8 kernel takes in one pass; otherwise the gate projection
   // into hf, then the up projection forming h from it
   const bool s16 = [](int t) { return t == QM_Q6_K || t == QM_IQ2_XS || t == QM_IQ2_S; }(gate->type);

@@ -82,10 +82,20 @@ struct MoeShared {
 };
 
 // MoE routing (qm_moe.hip); escale [NE] (or null): each chosen expert's weight times its scale
+// Tokens per wave of the routing kernel, and its work-groups (four waves each) for T tokens.
+// (about 2048 waves, two per SIMD: the selection is latency-bound, T = 4096 measured 20 us for the route + scan +
+// scatter chain at 2 tokens per wave, 23 at 4, 22 at 1)
+inline int moe_route_tpw(int T) { return T >= 4096 ? (T / 2048 < 16 ? T / 2048 : 16) : 1; }
+inline int moe_route_groups(int T) { return (T + 4 * moe_route_tpw(T) - 1) / (4 * moe_route_tpw(T)); }
+// counts (or null): per-expert counts by global atomics (counts zeroed first); part (or null): each work-group's
+// expert histogram as row blockIdx.x of part [moe_route_groups(T)][NE], plain stores
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
-                            const float* escale, hipStream_t s);
-hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s);
-hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int NE, int* cursor, int* stok,
+                            const float* escale, int* part, hipStream_t s);
+// From the routing histograms: counts; part's columns become running sums over the routing work-groups
+hipError_t launch_moe_scan(int* part, int groups, int* counts, int NE, hipStream_t s);
+// The slot permutation (stok, swt, inv) and the scan's outputs: first slots (cursor), tile starts, the tile list
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int T, int NU, int NE, const int* part,
+                              const int* counts, int* cursor, int* tstart, int* tiles, int tile_rows, int* stok,
                               float* swt, int* inv, hipStream_t s);
 hipError_t launch_moe_combine(float* x, const float* y, const int* inv, int T, int NU, int E, int accumulate,
                               const MoeShared& sh, hipStream_t s);

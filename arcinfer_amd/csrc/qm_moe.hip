@@ -7,17 +7,20 @@
 namespace qm {
 
 // One wave per token (each wave walks tpw tokens): the top NU of the NE logits by repeated arg-max (ties: the lower
-// expert), weights exp(l - max) / sum over the selection (summed in selection order; route_token). Per-expert counts go through
-// a work-group histogram in LDS and one global atomic per (work-group, expert), not one per (token, k): the router's
-// skew (Zipf) would otherwise serialise thousands of atomics on the popular experts' counters.
+// expert), weights exp(l - max) / sum over the selection (summed in selection order; route_token). Per-expert counts
+// go through a work-group histogram in LDS, then either one global atomic per (work-group, expert) (counts) or a
+// plain store of the histogram row (part; the tile path, whose scan sums the rows): the router's skew (Zipf) would
+// otherwise serialise thousands of atomics on the popular experts' counters.
 // zero/kernels/moe.cl:42-81 (moe_route), with 64-lane waves instead of 16-lane sub-groups.
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int ldl, int T, int NE, int NU,
-                                                    int tpw, int* __restrict__ ids, float* __restrict__ wts,
-                                                    int* __restrict__ counts, const float* __restrict__ escale) {
+                                                   int tpw, int* __restrict__ ids, float* __restrict__ wts,
+                                                   int* __restrict__ counts, const float* __restrict__ escale,
+                                                   int* __restrict__ part) {
   __shared__ int hist[64 * PER_LANE];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (counts)
+  const bool hst = counts || part;
+  if (hst)
     for (int e = threadIdx.x; e < NE; e += 256) hist[e] = 0;
   __syncthreads();
   // the next token's logits are loaded while the current one is selected
@@ -37,98 +40,170 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     if (lane < NU) {
       ids[(size_t)t * NU + lane] = my_e;
       wts[(size_t)t * NU + lane] = my_w;
-      if (counts) atomicAdd(&hist[my_e], 1);
+      if (hst) atomicAdd(&hist[my_e], 1);
     }
   }
-  if (counts) {
-    __syncthreads();
+  if (!hst) return;
+  __syncthreads();
+  if (part) {
+    for (int e = threadIdx.x; e < NE; e += 256) part[(size_t)blockIdx.x * NE + e] = hist[e];
+  } else {
     for (int e = threadIdx.x; e < NE; e += 256)
       if (hist[e]) atomicAdd(&counts[e], hist[e]);
   }
 }
 
 hipError_t launch_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* ids, float* wts, int* counts,
-                            const float* escale, hipStream_t s) {
-  // tokens per wave: enough work-groups to cover the CUs (about 1024 waves), more tokens each for large T
-  const int tpw = T >= 2048 ? min(16, T / 1024) : 1;
-  const dim3 grid((unsigned)((T + 4 * tpw - 1) / (4 * tpw))), block(256);
-  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
-  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
-  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale);
+                            const float* escale, int* part, hipStream_t s) {
+  // tokens per wave: moe_route_tpw (about 2048 waves; more tokens each for large T)
+  const int tpw = moe_route_tpw(T);
+  const dim3 grid((unsigned)moe_route_groups(T)), block(256);
+  if (NE <= 64) route_kernel<1><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale, part);
+  else if (NE <= 256) route_kernel<4><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale, part);
+  else route_kernel<16><<<grid, block, 0, s>>>(logits, ldl, T, NE, NU, tpw, ids, wts, counts, escale, part);
   return hipGetLastError();
 }
 
-// One work-group of NE threads: exclusive scans of the counts (slot offsets) and of the tile counts
-// (ceil(count / tile_rows)), then the tile list tiles[0] = #tiles, (expert, first slot, rows) per tile.
-// zero/kernels/moe.cl:133-160 (moe_scan).
-__global__ __launch_bounds__(1024) void scan_kernel(const int* __restrict__ counts, int* __restrict__ cursor,
-                                                    int* __restrict__ tstart, int* __restrict__ tiles, int NE,
-                                                    int tile_rows) {
-  __shared__ int sa[1024], sb[1024];
-  const int e = threadIdx.x;
-  const int c = e < NE ? counts[e] : 0, nt = (c + tile_rows - 1) / tile_rows;
-  sa[e] = c;
-  sb[e] = nt;
+// Work-group e (256 threads) sums expert e's column of the routing histograms part [G][NE] and rewrites it as
+// running sums (row g: how many of expert e's slots routing work-groups 0 .. g-1 took), then writes counts[e].
+__global__ __launch_bounds__(256) void scan_cols_kernel(int* __restrict__ part, int G, int* __restrict__ counts,
+                                                        int NE) {
+  __shared__ int red[256];
+  const int tid = threadIdx.x, e = blockIdx.x;
+  // this thread's rows [r0, r1): loaded at once (unconditional loads of clamped rows, zeroed past the range)
+  constexpr int RB = 8;
+  const int r0 = (int)((long long)tid * G / 256), r1 = (int)((long long)(tid + 1) * G / 256), nr = r1 - r0;
+  int v[RB], sum = 0;
+  const int rl = max(r1 - 1, 0);
+#pragma unroll
+  for (int k = 0; k < RB; ++k) v[k] = part[(size_t)min(r0 + k, rl) * NE + e];
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    v[k] = k < nr ? v[k] : 0;
+    sum += v[k];
+  }
+  for (int r = r0 + RB; r < r1; ++r) sum += part[(size_t)r * NE + e];  // (G > 2048 only)
+  red[tid] = sum;
   __syncthreads();
-  for (int d = 1; d < (int)blockDim.x; d <<= 1) {
-    const int x = e >= d ? sa[e - d] : 0, y = e >= d ? sb[e - d] : 0;
+  for (int d = 1; d < 256; d <<= 1) {
+    const int x = tid >= d ? red[tid - d] : 0;
     __syncthreads();
-    sa[e] += x;
-    sb[e] += y;
+    red[tid] += x;
     __syncthreads();
   }
-  if (e >= NE) return;
-  const int off = sa[e] - c, toff = sb[e] - nt;
-  cursor[e] = off;
-  tstart[e] = toff;
-  if (e == NE - 1) {
-    tiles[0] = sb[e];
-    tstart[NE] = sb[e];
+  int base = red[tid] - sum;  // the expert's slots taken by the rows before r0
+#pragma unroll
+  for (int k = 0; k < RB; ++k)
+    if (k < nr) {
+      part[(size_t)(r0 + k) * NE + e] = base;
+      base += v[k];
+    }
+  for (int r = r0 + RB; r < r1; ++r) {
+    int* q = part + (size_t)r * NE + e;
+    const int x = *q;
+    *q = base;
+    base += x;
   }
-  for (int i = 0; i < nt; ++i) {
-    int* tp = tiles + 1 + 3 * (toff + i);
-    tp[0] = e;
-    tp[1] = off + i * tile_rows;
-    tp[2] = min(tile_rows, c - i * tile_rows);
-  }
+  if (tid == 255) counts[e] = red[255];
 }
 
-hipError_t launch_moe_scan(int* counts, int* cursor, int* tstart, int* tiles, int NE, int tile_rows, hipStream_t s) {
-  int threads = 64;
-  while (threads < NE) threads <<= 1;
-  scan_kernel<<<1, threads, 0, s>>>(counts, cursor, tstart, tiles, NE, tile_rows);
+hipError_t launch_moe_scan(int* part, int groups, int* counts, int NE, hipStream_t s) {
+  if (NE > 1024) return hipErrorInvalidValue;
+  scan_cols_kernel<<<NE, 256, 0, s>>>(part, groups, counts, NE);
   return hipGetLastError();
 }
 
 // Every (token, k) pair takes the next slot of its expert: slot order within an expert is arbitrary, so every
-// consumer works per slot and the combine reads the slots back through inv in k order. A work-group ranks its 256
-// pairs per expert in LDS, reserves each expert's range with one global atomic, then writes the slots.
-// zero/kernels/moe.cl:163-171 (moe_scatter).
-__global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ ids, const float* __restrict__ wts, int n,
-                                                      int NU, int NE, int* __restrict__ cursor, int* __restrict__ stok,
+// consumer works per slot and the combine reads the slots back through inv in k order. Each work-group first scans
+// the counts in LDS (exclusive scans of the counts: first slots; of the tile counts ceil(count / tile_rows): tile
+// starts); work-group 0 writes those (cursor, tstart) and every work-group a share of the tile list tiles[0] =
+// #tiles, (expert, first slot, rows) per tile, tile i found by a binary search of the tile prefix
+// (zero/kernels/moe.cl:133-160, moe_scan). Then work-group g takes the pairs of routing work-group g's tokens, ranks
+// them per expert in LDS and adds the ranks to the expert's first slot and the slots the routing work-groups before g
+// took (row g of part, as scan_cols_kernel left it): no global atomics. zero/kernels/moe.cl:163-171 (moe_scatter).
+__global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ ids, const float* __restrict__ wts,
+                                                      int n, int per_group, int NU, int NE,
+                                                      const int* __restrict__ part, const int* __restrict__ counts,
+                                                      int* __restrict__ cursor, int* __restrict__ tstart,
+                                                      int* __restrict__ tiles, int tile_rows, int* __restrict__ stok,
                                                       float* __restrict__ swt, int* __restrict__ inv) {
-  extern __shared__ int sh[];
-  int* cnt = sh;        // [NE] pairs of this work-group per expert
-  int* base = sh + NE;  // [NE] first slot reserved for them
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  for (int e = threadIdx.x; e < NE; e += blockDim.x) cnt[e] = 0;
+  __shared__ int ra[256], rb[256], sa[1024], sb[1024], cnt[1024];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < NE; e += 256) cnt[e] = 0;
+  const int per = (NE + 255) / 256;  // experts per thread, consecutive (NE <= 1024)
+  int c4[4], n4[4], cs = 0, ns = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int x = tid * per + k;
+    c4[k] = k < per && x < NE ? counts[x] : 0;
+    n4[k] = (c4[k] + tile_rows - 1) / tile_rows;
+    cs += c4[k];
+    ns += n4[k];
+  }
+  ra[tid] = cs;
+  rb[tid] = ns;
   __syncthreads();
-  const int e = i < n ? ids[i] : 0;
-  const int r = i < n ? atomicAdd(&cnt[e], 1) : 0;
+  for (int d = 1; d < 256; d <<= 1) {
+    const int x = tid >= d ? ra[tid - d] : 0, y = tid >= d ? rb[tid - d] : 0;
+    __syncthreads();
+    ra[tid] += x;
+    rb[tid] += y;
+    __syncthreads();
+  }
+  int co = ra[tid] - cs, no = rb[tid] - ns;  // exclusive prefixes at this thread's first expert
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int x = tid * per + k;
+    if (k < per && x < NE) {
+      if (blockIdx.x == 0) {
+        cursor[x] = co;
+        tstart[x] = no;
+      }
+      co += c4[k];
+      no += n4[k];
+      sa[x] = co;  // inclusive prefixes over experts
+      sb[x] = no;
+    }
+  }
   __syncthreads();
-  for (int x = threadIdx.x; x < NE; x += blockDim.x)
-    if (cnt[x]) base[x] = atomicAdd(&cursor[x], cnt[x]);
-  __syncthreads();
-  if (i >= n) return;
-  const int slot = base[e] + r;
-  stok[slot] = i / NU;
-  swt[slot] = wts[i];
-  inv[i] = slot;
+  const int ntot = sb[NE - 1];
+  if (blockIdx.x == 0 && tid == 0) {
+    tiles[0] = ntot;
+    tstart[NE] = ntot;
+  }
+  // this work-group's share of the tile list: tile i belongs to the first expert whose inclusive tile prefix exceeds i
+  for (int i = blockIdx.x * 256 + tid; i < ntot; i += gridDim.x * 256) {
+    int lo = 0, hi = NE;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sb[mid] > i) hi = mid;
+      else lo = mid + 1;
+    }
+    const int x = lo, first = x == 0 ? 0 : sa[x - 1], cx = sa[x] - first, k = i - (x == 0 ? 0 : sb[x - 1]);
+    int* tp = tiles + 1 + 3 * i;
+    tp[0] = x;
+    tp[1] = first + k * tile_rows;
+    tp[2] = min(tile_rows, cx - k * tile_rows);
+  }
+  // the slots
+  const int i0 = blockIdx.x * per_group, i1 = min(n, i0 + per_group);
+  const int* base = part + (size_t)blockIdx.x * NE;
+  for (int i = i0 + tid; i < i1; i += 256) {
+    const int e = ids[i];
+    const int slot = (e == 0 ? 0 : sa[e - 1]) + base[e] + atomicAdd(&cnt[e], 1);
+    stok[slot] = i / NU;
+    swt[slot] = wts[i];
+    inv[i] = slot;
+  }
 }
 
-hipError_t launch_moe_scatter(const int* ids, const float* wts, int n, int NU, int NE, int* cursor, int* stok,
+hipError_t launch_moe_scatter(const int* ids, const float* wts, int T, int NU, int NE, const int* part,
+                              const int* counts, int* cursor, int* tstart, int* tiles, int tile_rows, int* stok,
                               float* swt, int* inv, hipStream_t s) {
-  scatter_kernel<<<(n + 255) / 256, 256, 2 * sizeof(int) * NE, s>>>(ids, wts, n, NU, NE, cursor, stok, swt, inv);
+  if (NE > 1024) return hipErrorInvalidValue;
+  const int per_group = 4 * moe_route_tpw(T) * NU;
+  scatter_kernel<<<moe_route_groups(T), 256, 0, s>>>(ids, wts, T * NU, per_group, NU, NE, part, counts, cursor, tstart,
+                                                     tiles, tile_rows, stok, swt, inv);
   return hipGetLastError();
 }
 

@@ -286,7 +286,7 @@ hipError_t launch_moe_decode(int tg, int tu, int td, const WView& gate, const WV
   if (T > 4 || tg != tu) {
     // (more tokens: every gate/up work-group routing its token in front of its weight loads costs more than a
     //  separate route launch, measured at T = 8; two gate/up launches route once, here)
-    const hipError_t e = launch_moe_route(logits, ldl, T, NE, NU, ids, wts, nullptr, escale, s);
+    const hipError_t e = launch_moe_route(logits, ldl, T, NE, NU, ids, wts, nullptr, escale, nullptr, s);
     if (e != hipSuccess) return e;
     logits = nullptr;
   }

@@ -104,6 +104,32 @@ def moe_check(qm, s, types, NE, E, Fd, T, NU, tokens=None, escale=None, sh=None,
     assert rel_err(got[list(toks)], ref) < 1e-4
 
 
+def check_permutation(qm, s, NE, E, Fd, T, NU):
+    """The tile path's routing state in the workspace: slots of each expert contiguous, a bijection onto (token, k);
+    the scan's counts, first slots, tile starts and tile list."""
+    L = qm.moe_ws_layout(T, NE, NU, E, Fd)
+    ws = s["ws"].cpu().numpy()
+    view = lambda off, n, dt: np.frombuffer(ws[off:off + n * np.dtype(dt).itemsize].tobytes(), dtype=dt)
+    ids = view(L.ids, T * NU, np.int32)
+    inv = view(L.inv, T * NU, np.int32)
+    stok = view(L.stok, T * NU, np.int32)
+    assert np.array_equal(np.sort(inv), np.arange(T * NU))
+    assert np.array_equal(stok[inv], np.arange(T * NU) // NU)
+    counts = np.bincount(ids, minlength=NE)
+    offs = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    assert np.all((offs[ids] <= inv) & (inv < offs[ids] + counts[ids]))
+    tiles = view(L.tiles, 1 + 3 * L.max_tiles, np.int32)
+    assert tiles[0] == int(np.sum((counts + L.tile_rows - 1) // L.tile_rows))
+    # the scan's outputs: counts, first slots, tile starts and the whole tile list
+    assert np.array_equal(view(L.counts, NE, np.int32), counts)
+    assert np.array_equal(view(L.cursor, NE, np.int32), offs)
+    nt = (counts + L.tile_rows - 1) // L.tile_rows
+    assert np.array_equal(view(L.tstart, NE + 1, np.int32), np.concatenate([[0], np.cumsum(nt)]))
+    want = [(e, offs[e] + k * L.tile_rows, min(L.tile_rows, counts[e] - k * L.tile_rows))
+            for e in range(NE) for k in range(nt[e])]
+    assert np.array_equal(tiles[1:1 + 3 * len(want)].reshape(-1, 3), np.array(want, dtype=np.int32).reshape(-1, 3))
+
+
 @pytest.mark.parametrize("qtype,NE,E,Fd,T,NU", [(F.IQ4_XS, 16, 512, 256, 64, 4), (F.IQ3_S, 8, 256, 512, 40, 2),
                                                 (F.Q8_0, 8, 256, 256, 9, 3), (F.IQ4_XS, 256, 2048, 512, 48, 8),
                                                 (F.Q4_0, 8, 256, 256, 70, 2), (F.IQ4_NL, 16, 512, 256, 33, 4),
@@ -116,22 +142,19 @@ def test_moe_grouped_matches_oracle(qm, dev, qtype, NE, E, Fd, T, NU):
     moe_check(qm, s, (qtype,) * 3, NE, E, Fd, T, NU)
     if T * NU <= 64:
         return  # (decode sizes take the GEMV-shaped kernels: no slot permutation is built)
-    # the device permutation: slots of each expert contiguous, a bijection onto (token, k)
-    L = qm.moe_ws_layout(T, NE, NU, E, Fd)
-    ws = s["ws"].cpu().numpy()
-    view = lambda off, n, dt: np.frombuffer(ws[off:off + n * np.dtype(dt).itemsize].tobytes(), dtype=dt)
-    ids = view(L.ids, T * NU, np.int32)
-    inv = view(L.inv, T * NU, np.int32)
-    stok = view(L.stok, T * NU, np.int32)
-    assert np.array_equal(np.sort(inv), np.arange(T * NU))
-    assert np.array_equal(stok[inv], np.arange(T * NU) // NU)
-    counts = np.bincount(ids, minlength=NE)
-    offs = np.concatenate([[0], np.cumsum(counts)[:-1]])
-    for i in range(T * NU):
-        e = ids[i]
-        assert offs[e] <= inv[i] < offs[e] + counts[e]
-    tiles = view(L.tiles, 1 + 3 * L.max_tiles, np.int32)
-    assert tiles[0] == int(np.sum((counts + L.tile_rows - 1) // L.tile_rows))
+    check_permutation(qm, s, NE, E, Fd, T, NU)
+
+
+def test_moe_routing_state_large_T(qm, dev):
+    """T >= 2048: several tokens per routing wave, the scatter's work-groups following the routing work-groups, a
+    ragged last group (T not a multiple of the group's tokens); outputs checked on a few tokens."""
+    import torch
+    NE, E, Fd, T, NU = 64, 256, 256, 4100, 6
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=11)
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    torch.cuda.synchronize()
+    check_permutation(qm, s, NE, E, Fd, T, NU)
+    moe_check(qm, s, (F.IQ4_XS,) * 3, NE, E, Fd, T, NU, tokens=[0, 1, 2047, 2048, 4095, 4096, 4099])
 
 
 def test_moe_accumulate_and_determinism(qm, dev):
