@@ -8,7 +8,6 @@
 // the reference's expression `sa * d * (float)(sc0 * lo + sc1 * hi)` (zero/kernels/decode.cl:695-706, 1107-1115),
 // with the min term for Q4_K. A cross-lane butterfly then sums the group's partial results.
 #pragma once
-#include <stdlib.h>
 
 #include "qm_decode.h"
 

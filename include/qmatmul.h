@@ -189,7 +189,11 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
                            int M_stride, const float* escale, const float* sh, int ldsh, int sh_gated, float* x,
                            int accumulate, void* ws, size_t ws_bytes, void* stream);
 
-/* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). */
+/* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). After a tile-path call
+ * (T * NU > 64): ids / wts the routing; counts[e] the slots of expert e; cursor[e] its first slot; tstart[e] its first
+ * tile (tstart[NE] = the tile count); tiles[0] = the tile count, then (expert, first slot, rows) per tile; stok / swt
+ * each slot's token and routing weight; inv[t * NU + k] the slot of (token t, pick k). The workspace also holds
+ * internal routing histograms after hf (inside total). */
 typedef struct {
   size_t ids, wts, counts, cursor, tstart, tiles, stok, swt, inv, hq, hsc, y, hf, total;
   int slots, max_tiles, tile_rows;
