@@ -157,6 +157,17 @@ def test_moe_routing_state_large_T(qm, dev):
     moe_check(qm, s, (F.IQ4_XS,) * 3, NE, E, Fd, T, NU, tokens=[0, 1, 2047, 2048, 4095, 4096, 4099])
 
 
+def test_moe_routing_state_many_experts(qm, dev):
+    """NE = 600 (not a power of two, above 512: three experts per thread in the scatter's expert scan), tile path."""
+    import torch
+    NE, E, Fd, T, NU = 600, 256, 256, 300, 4
+    s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=13)
+    qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+    torch.cuda.synchronize()
+    check_permutation(qm, s, NE, E, Fd, T, NU)
+    moe_check(qm, s, (F.IQ4_XS,) * 3, NE, E, Fd, T, NU, tokens=[0, 1, 150, 299])
+
+
 def test_moe_accumulate_and_determinism(qm, dev):
     import torch
     NE, E, Fd, T, NU = 32, 256, 256, 100, 4
