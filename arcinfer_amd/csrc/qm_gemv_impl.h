@@ -407,9 +407,10 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
         if (a.dbg_msum) c.dbg_msum = a.dbg_msum + (size_t)t0 * a.w.rows * nb;
       }
       hipError_t e;
-      if (a.T == 1 && nb <= 256 && a.w.rows <= 6144) {
-        // batch 1, a small matrix (the grid has about one row per 32-lane group): 128 lanes per row, token blocks in
-        // registers, three work-groups per CU. Measured against 32 lanes per row: Q8_0 4096 x 4096 6.8 -> 6.4 us,
+      if (a.T == 1 && nb > 64 && nb <= 256 && a.w.rows <= 6144) {
+        // batch 1, a small matrix (the grid has about one row per 32-lane group) with rows of more than 64 blocks (so
+        // at least half of the 128 lanes have a block): 128 lanes per row, token blocks in registers, three
+        // work-groups per CU. Measured against 32 lanes per row: Q8_0 4096 x 4096 6.8 -> 6.4 us,
         // IQ3_S 5120 x 5120 7.7 -> 6.8 us, IQ4_XS 5120 x 5120 6.7 -> 6.2 us
         e = nb <= 128 ? gos<TYPE, 128, 1, false, 1, DUMP, true, 3>(c, s) : gos<TYPE, 128, 2, false, 1, DUMP, true, 3>(c, s);
       } else if (a.T == 1 && nb > 512 && nb <= 768) {
