@@ -107,7 +107,7 @@ MoeLayout moe_layout(int T, int NE, int NU, int E, int F) {
   MoeLayout L;
   L.slots = T * NU;
   L.tile_rows = qm::kMoeTileRows;
-  L.max_tiles = (L.slots + qm::kMoeTileRows - 1) / qm::kMoeTileRows + NE;
+  L.max_tiles = (L.slots + qm::kMoeTileRows - 1) / qm::kMoeTileRows + 2 * NE;  // (+ one even-ing entry per expert)
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;

@@ -236,6 +236,18 @@ __device__ __forceinline__ bool tile_rows(const GemmArgs& a, int& m0, int& nvali
     nvalid = min(BM, a.M - m0);
     wrow0 = 0;
     return true;
+  } else if constexpr (BM > kMoeTileRows) {
+    // two consecutive tiles of one expert (the tile list starts every expert's tiles at an even index, the second
+    // of a pair possibly empty)
+    const int t = 2 * (int)blockIdx.y;
+    if (t >= a.tiles[0]) return false;
+    const int e = a.tiles[1 + 3 * t];
+    m0 = a.tiles[2 + 3 * t];
+    nvalid = a.tiles[3 + 3 * t] + (t + 1 < a.tiles[0] ? a.tiles[3 + 3 * (t + 1)] : 0);
+    if (nvalid <= 0) return false;
+    wrow0 = e * a.expert_rows;
+    nt = blockIdx.x;
+    return true;
   } else {
     constexpr int SUB = kMoeTileRows / BM;
     const int t = blockIdx.y / SUB, sub = blockIdx.y % SUB;
@@ -321,14 +333,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   }
   // ---- this lane's weight row: payloads and header, one superblock ahead (rolling: a block's registers are
   // reloaded with the next superblock's block as soon as they are consumed)
-  uint4 pay[8], pay2[GU ? 8 : 1];
+  // (gate and up over two slot tiles: a ring of four blocks, two block pairs ahead, for the registers; the types whose
+  //  block scales sit in the payloads need the whole superblock at its start)
+  constexpr int NP = GU && MT == 2 ? 4 : 8;
+  static_assert(NP == 8 || (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS), "payload-held scales need the whole superblock");
+  uint4 pay[NP], pay2[GU ? NP : 1];
   uint4 hdr, hdr2 = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) pay[b] = load_payload<TYPE>(a.w, n, sb0 * 8 + b, hf);
+  for (int b = 0; b < NP; ++b) pay[b] = load_payload<TYPE>(a.w, n, sb0 * 8 + b, hf);
   hdr = load_header<TYPE>(a.w, n, sb0);
   if constexpr (GU) {
 #pragma unroll
-    for (int b = 0; b < 8; ++b) pay2[b] = load_payload<TYPE>(a.w2, n, sb0 * 8 + b, hf);
+    for (int b = 0; b < NP; ++b) pay2[b] = load_payload<TYPE>(a.w2, n, sb0 * 8 + b, hf);
     hdr2 = load_header<TYPE>(a.w2, n, sb0);
   }
 
@@ -384,12 +400,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       v4i bop[2], bop2[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int b = 2 * p + q;
-        bop[q] = b_operand<TYPE>(pay[b], hcur, b, hf, kv, &L.tab);
-        pay[b] = load_payload<TYPE>(a.w, n, sn * 8 + b, hf);
+        const int b = 2 * p + q, sl = b % NP;
+        // the block that takes this slot: the next superblock's block b, or (ring of four) block b + 4 of this one
+        // for the first two pairs and block b - 4 of the next for the last two
+        const int bn = NP == 8 ? sn * 8 + b : (p < 2 ? s * 8 + b + 4 : sn * 8 + b - 4);
+        bop[q] = b_operand<TYPE>(pay[sl], hcur, b, hf, kv, &L.tab);
+        pay[sl] = load_payload<TYPE>(a.w, n, bn, hf);
         if constexpr (GU) {
-          bop2[q] = b_operand<TYPE>(pay2[b], hcur2, b, hf, kv, &L.tab);
-          pay2[b] = load_payload<TYPE>(a.w2, n, sn * 8 + b, hf);
+          bop2[q] = b_operand<TYPE>(pay2[sl], hcur2, b, hf, kv, &L.tab);
+          pay2[sl] = load_payload<TYPE>(a.w2, n, bn, hf);
         }
       }
       if constexpr (MODE == GEMM_DENSE && MT == 2) {
@@ -437,6 +456,38 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
           }
         }
+        }
+      } else if constexpr (GU && MT == 2 && !DUMP) {
+        // two slot tiles share each decoded weight operand; per tile the gate part, then the up part (one pair of
+        // MFMA results and one outer product live at a time); a tile with no slots (a half-empty pair) is skipped
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          if (mt > 0 && nvalid <= 32) break;
+          __builtin_amdgcn_sched_barrier(0);
+          v4i aop[2];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const uint4 av = *(const uint4*)(L.a[cur] + (mt * 32 + lc) * A_STRIDE + 32 * (2 * p + q) + 16 * hf);
+            aop[q] = v4i{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+          }
+          const float my_asc = L.asc[cur][(2 * p + hf) * BM + mt * 32 + lc];
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            v16i dv[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+              dv[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[q], g ? bop2[q] : bop[q], zero16, 0, 0, 0);
+            const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(my_asc, g ? my_dsc2 : my_dsc, zero32, 0, 0, 0);
+            v16f& ac = g ? acc2[mt] : acc[mt];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              ac[r] = fmaf(sc[r], (float)dv[0][r], ac[r]);
+              ac[r] = fmaf(sc[16 + r], (float)dv[1][r], ac[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(ac[r]));
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       } else
 #pragma unroll
@@ -765,14 +816,14 @@ __global__ __launch_bounds__(256, 2) void moe_down_rw_kernel(GemmArgs a, int gro
 #pragma unroll
     for (int c = 0; c < ACH; ++c) {
       const int ch = tid + 256 * c, row = ch / (F / 16), col = ch % (F / 16);
-      st_a[c] = *(const u32x4_t*)(a.aq + (size_t)(m0 + min(row, nr - 1)) * F + col * 16);
+      st_a[c] = *(const u32x4_t*)(a.aq + (size_t)(m0 + min(row, max(nr, 1) - 1)) * F + col * 16);
     }
 #pragma unroll
     for (int c = 0; c < SCH; ++c) {
       const int idx = min(tid + 256 * c, NB * 32 - 1), blk = idx >> 5, row = idx & 31;
-      st_sc[c] = a.asc[(size_t)blk * a.M_stride + m0 + min(row, nr - 1)];
+      st_sc[c] = a.asc[(size_t)blk * a.M_stride + m0 + min(row, max(nr, 1) - 1)];
     }
-    if (tid < 32) st_rs = a.rowscale[m0 + min(tid, nr - 1)];
+    if (tid < 32) st_rs = a.rowscale[m0 + min(tid, max(nr, 1) - 1)];
   };
 
   v4i bop[NB];
@@ -813,6 +864,7 @@ __global__ __launch_bounds__(256, 2) void moe_down_rw_kernel(GemmArgs a, int gro
     }
     __syncthreads();
     if (t + 1 < t1) fetch(t + 1);  // (the next tile's loads fly during this tile's MFMAs)
+    if (nr == 0) continue;  // (an empty tile: the second of an expert's last pair)
     v16f acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -876,8 +928,9 @@ template <int TYPE, int MT, int MODE, bool DUMP>
 static hipError_t go(const GemmArgs& a, hipStream_t s) {
   const int n_rows = MODE == GEMM_DENSE ? a.w.rows : a.expert_rows;
   const unsigned gx = (unsigned)((n_rows + 127) / 128);
-  const unsigned gy = MODE == GEMM_DENSE ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT))
-                                          : (unsigned)(a.max_tiles * (kMoeTileRows / (32 * MT)));
+  const unsigned gy = MODE == GEMM_DENSE      ? (unsigned)((a.M + 32 * MT - 1) / (32 * MT))
+                     : 32 * MT > kMoeTileRows ? (unsigned)((a.max_tiles + 1) / 2)
+                                              : (unsigned)(a.max_tiles * (kMoeTileRows / (32 * MT)));
   // A dense product with too few tiles to give every CU two work-groups (M = 512, N = 5120: 320 tiles) splits K in two:
   // each half adds its partial sums into a zeroed C, so the grid doubles. Two partials keep the result deterministic
   // (0 + x + y rounds the same in either order); only with accumulate = 0 (C + x + y would not).
@@ -898,7 +951,10 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
   switch (mode) {
     case GEMM_DENSE:
       return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
-    case GEMM_MOE_GATEUP: return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
+    case GEMM_MOE_GATEUP:
+      // (IQ4_XS: two slot tiles per work-group, each decoded weight operand feeding both)
+      if constexpr (TYPE == T_IQ4_XS) return go<TYPE, 2, GEMM_MOE_GATEUP, false>(a, s);
+      return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN:
       // (expert width F <= 512: the whole row's operands fit in registers; types with mins are not MoE types)
       if constexpr (!Traits<TYPE>::MINS) {

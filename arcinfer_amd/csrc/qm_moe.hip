@@ -115,9 +115,10 @@ hipError_t launch_moe_scan(int* part, int groups, int* counts, int NE, hipStream
 
 // Every (token, k) pair takes the next slot of its expert: slot order within an expert is arbitrary, so every
 // consumer works per slot and the combine reads the slots back through inv in k order. Each work-group first scans
-// the counts in LDS (exclusive scans of the counts: first slots; of the tile counts ceil(count / tile_rows): tile
-// starts); work-group 0 writes those (cursor, tstart) and every work-group a share of the tile list tiles[0] =
-// #tiles, (expert, first slot, rows) per tile, tile i found by a binary search of the tile prefix
+// the counts in LDS (exclusive scans of the counts: first slots; of the tile counts ceil(count / tile_rows), rounded
+// up to even so every expert's tiles start at an even index and pair up: tile starts); work-group 0 writes those
+// (cursor, tstart) and every work-group a share of the tile list tiles[0] = #entries, (expert, first slot, rows) per
+// entry (an odd count's extra entry: 0 rows, at the expert's last slot), entry i found by a binary search
 // (zero/kernels/moe.cl:133-160, moe_scan). Then work-group g takes the pairs of routing work-group g's tokens, ranks
 // them per expert in LDS and adds the ranks to the expert's first slot and the slots the routing work-groups before g
 // took (row g of part, as scan_cols_kernel left it): no global atomics. zero/kernels/moe.cl:163-171 (moe_scatter).
@@ -137,6 +138,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ id
     const int x = tid * per + k;
     c4[k] = k < per && x < NE ? counts[x] : 0;
     n4[k] = (c4[k] + tile_rows - 1) / tile_rows;
+    n4[k] += n4[k] & 1;  // (an even number of tile entries per expert: the gate/up kernel takes tiles in pairs)
     cs += c4[k];
     ns += n4[k];
   }
@@ -181,9 +183,10 @@ __global__ __launch_bounds__(256) void scatter_kernel(const int* __restrict__ id
     }
     const int x = lo, first = x == 0 ? 0 : sa[x - 1], cx = sa[x] - first, k = i - (x == 0 ? 0 : sb[x - 1]);
     int* tp = tiles + 1 + 3 * i;
+    const bool pad = k * tile_rows >= cx;  // (the empty entry that evens an odd tile count: at the last slot)
     tp[0] = x;
-    tp[1] = first + k * tile_rows;
-    tp[2] = min(tile_rows, cx - k * tile_rows);
+    tp[1] = pad ? first + cx - 1 : first + k * tile_rows;
+    tp[2] = pad ? 0 : min(tile_rows, cx - k * tile_rows);
   }
   // the slots
   const int i0 = blockIdx.x * per_group, i1 = min(n, i0 + per_group);

@@ -191,7 +191,8 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
 
 /* Byte offsets of the MoE workspace's arrays (for tests and tools reading the routing state). After a tile-path call
  * (T * NU > 64): ids / wts the routing; counts[e] the slots of expert e; cursor[e] its first slot; tstart[e] its first
- * tile (tstart[NE] = the tile count); tiles[0] = the tile count, then (expert, first slot, rows) per tile; stok / swt
+ * tile (tstart[NE] = the tile count); tiles[0] = the tile count, then (expert, first slot, rows) per tile, every
+ * expert's tiles starting at an even index (an odd count gets one more entry of 0 rows at its last slot); stok / swt
  * each slot's token and routing weight; inv[t * NU + k] the slot of (token t, pick k). The workspace also holds
  * internal routing histograms after hf (inside total). */
 typedef struct {

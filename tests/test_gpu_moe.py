@@ -119,14 +119,16 @@ def check_permutation(qm, s, NE, E, Fd, T, NU):
     offs = np.concatenate([[0], np.cumsum(counts)[:-1]])
     assert np.all((offs[ids] <= inv) & (inv < offs[ids] + counts[ids]))
     tiles = view(L.tiles, 1 + 3 * L.max_tiles, np.int32)
-    assert tiles[0] == int(np.sum((counts + L.tile_rows - 1) // L.tile_rows))
+    ntl = (counts + L.tile_rows - 1) // L.tile_rows
+    assert tiles[0] == int(np.sum(ntl + (ntl & 1)))
     # the scan's outputs: counts, first slots, tile starts and the whole tile list
     assert np.array_equal(view(L.counts, NE, np.int32), counts)
     assert np.array_equal(view(L.cursor, NE, np.int32), offs)
     nt = (counts + L.tile_rows - 1) // L.tile_rows
-    assert np.array_equal(view(L.tstart, NE + 1, np.int32), np.concatenate([[0], np.cumsum(nt)]))
-    want = [(e, offs[e] + k * L.tile_rows, min(L.tile_rows, counts[e] - k * L.tile_rows))
-            for e in range(NE) for k in range(nt[e])]
+    npad = nt + (nt & 1)  # (each expert's tiles start at an even index: an odd count gets an empty entry)
+    assert np.array_equal(view(L.tstart, NE + 1, np.int32), np.concatenate([[0], np.cumsum(npad)]))
+    want = [(e, offs[e] + k * L.tile_rows, min(L.tile_rows, counts[e] - k * L.tile_rows)) if k < nt[e]
+            else (e, offs[e] + counts[e] - 1, 0) for e in range(NE) for k in range(npad[e])]
     assert np.array_equal(tiles[1:1 + 3 * len(want)].reshape(-1, 3), np.array(want, dtype=np.int32).reshape(-1, 3))
 
 
