@@ -952,8 +952,9 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
     case GEMM_DENSE:
       return a.M <= 32 ? go<TYPE, 1, GEMM_DENSE, false>(a, s) : go<TYPE, 2, GEMM_DENSE, false>(a, s);
     case GEMM_MOE_GATEUP:
-      // (IQ4_XS: two slot tiles per work-group, each decoded weight operand feeding both)
-      if constexpr (TYPE == T_IQ4_XS) return go<TYPE, 2, GEMM_MOE_GATEUP, false>(a, s);
+      // (two slot tiles per work-group, each decoded weight operand feeding both; IQ2_XXS / IQ3_XXS keep their block
+      //  scales in the payloads, which the two-tile kernel's payload ring does not hold whole)
+      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS) return go<TYPE, 2, GEMM_MOE_GATEUP, false>(a, s);
       return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN:
       // (expert width F <= 512: the whole row's operands fit in registers; types with mins are not MoE types)
