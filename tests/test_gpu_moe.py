@@ -135,7 +135,9 @@ def check_permutation(qm, s, NE, E, Fd, T, NU):
 @pytest.mark.parametrize("qtype,NE,E,Fd,T,NU", [(F.IQ4_XS, 16, 512, 256, 64, 4), (F.IQ3_S, 8, 256, 512, 40, 2),
                                                 (F.Q8_0, 8, 256, 256, 9, 3), (F.IQ4_XS, 256, 2048, 512, 48, 8),
                                                 (F.Q4_0, 8, 256, 256, 70, 2), (F.IQ4_NL, 16, 512, 256, 33, 4),
-                                                (F.IQ2_XXS, 8, 512, 256, 40, 2), (F.IQ3_XXS, 16, 256, 512, 33, 4)])
+                                                (F.IQ2_XXS, 8, 512, 256, 40, 2), (F.IQ3_XXS, 16, 256, 512, 33, 4),
+                                                (F.IQ4_XS, 16, 512, 768, 40, 4), (F.Q8_0, 8, 256, 1024, 40, 4),
+                                                (F.IQ3_XXS, 8, 256, 1024, 30, 4)])
 def test_moe_grouped_matches_oracle(qm, dev, qtype, NE, E, Fd, T, NU):
     import torch
     s = _moe_setup(qm, dev, NE, E, Fd, T, NU, qtype, seed=NE + T)
