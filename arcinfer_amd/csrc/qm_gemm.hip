@@ -968,17 +968,13 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
         //  against two slot tiles per work-group in the tile kernel)
         if (a.w.K == 768) return go_down_rw<TYPE, 3>(a, s);
       }
-      // wider experts: two slot tiles per work-group (0.88 -> 0.85 ms at F = 768), except the payload-scale types
-      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS) return go<TYPE, 2, GEMM_MOE_DOWN, false>(a, s);
-      return go<TYPE, 1, GEMM_MOE_DOWN, false>(a, s);
+      // wider experts (and the payload-scale types IQ2_XXS / IQ3_XXS): two slot tiles per work-group (0.88 -> 0.85 ms
+      // at F = 768)
+      return go<TYPE, 2, GEMM_MOE_DOWN, false>(a, s);
     // (gate and up of different types: each launch over slot-tile pairs as well; measured 227 -> 181 us for the gate
     //  launch at the BASELINE MoE shape)
-    case GEMM_MOE_G:
-      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS) return go<TYPE, 2, GEMM_MOE_G, false>(a, s);
-      return go<TYPE, 1, GEMM_MOE_G, false>(a, s);
-    case GEMM_MOE_UH:
-      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS) return go<TYPE, 2, GEMM_MOE_UH, false>(a, s);
-      return go<TYPE, 1, GEMM_MOE_UH, false>(a, s);
+    case GEMM_MOE_G: return go<TYPE, 2, GEMM_MOE_G, false>(a, s);
+    case GEMM_MOE_UH: return go<TYPE, 2, GEMM_MOE_UH, false>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
