@@ -61,6 +61,12 @@ int header_bytes(int t) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// the types of 32-element blocks, whose rows may end inside a superblock (padded with zero blocks when prepared)
+bool small_block_type(int t) { return t == QM_Q8_0 || t == QM_Q4_0 || t == QM_IQ4_NL; }
+bool row_length_ok(int t, int K) { return K > 0 && (K % 256 == 0 || (small_block_type(t) && K % 32 == 0)); }
+int padded_k(int K) { return (K + 255) / 256 * 256; }
+
+
 size_t plane_qs_bytes(int t, int rows, int K) { return (size_t)rows * (K / 32) * payload_bytes(t); }
 size_t plane_hdr_bytes(int t, int rows, int K) { return (size_t)rows * (K / 256) * header_bytes(t); }
 
@@ -162,7 +168,8 @@ size_t qmatmul_sb_bytes(int type) {
 }
 
 size_t qmatmul_weight_bytes(int type, int rows, int K) {
-  if (!known_type(type) || rows <= 0 || K <= 0 || K % 256) return 0;
+  if (!known_type(type) || rows <= 0 || !row_length_ok(type, K)) return 0;
+  K = padded_k(K);
   return align256(plane_qs_bytes(type, rows, K)) + plane_hdr_bytes(type, rows, K);
 }
 
@@ -171,12 +178,17 @@ int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int row
   if (!out || !raw) return fail(QM_ERR_ARG, "qmatmul_prepare_weight: null pointer");
   *out = nullptr;
   if (!known_type(type)) return fail(QM_ERR_TYPE, "qmatmul_prepare_weight: unsupported type %d", type);
-  if (rows <= 0 || K <= 0 || K % 256)
-    return fail(QM_ERR_SHAPE, "qmatmul_prepare_weight: rows %d, K %d (K must be a positive multiple of 256)", rows, K);
+  if (rows <= 0 || !row_length_ok(type, K))
+    return fail(QM_ERR_SHAPE,
+                "qmatmul_prepare_weight: rows %d, K %d (K must be a positive multiple of 256, or of 32 for Q8_0, "
+                "Q4_0 and IQ4_NL)", rows, K);
   QM_CHECK_INIT();
   hipStream_t s = (hipStream_t)stream;
+  const int kraw = K / 32;  // 32-blocks per raw row
+  const size_t rawb = small_block_type(type) ? (size_t)rows * kraw * (qmatmul_sb_bytes(type) / 8)
+                                             : (size_t)rows * (K / 256) * qmatmul_sb_bytes(type);
+  K = padded_k(K);  // (the prepared row: zero blocks up to whole superblocks)
   const size_t qsb = plane_qs_bytes(type, rows, K), total = qmatmul_weight_bytes(type, rows, K);
-  const size_t rawb = (size_t)rows * (K / 256) * qmatmul_sb_bytes(type);
   qm_weight* w = new (std::nothrow) qm_weight();
   if (!w) return fail(QM_ERR_NOMEM, "qmatmul_prepare_weight: host allocation");
   hipError_t e = hipGetDevice(&w->device);
@@ -210,7 +222,7 @@ int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int row
   w->view.hdr = w->base + align256(qsb);
   w->view.rows = rows;
   w->view.K = K;
-  e = qm::launch_repack(type, src, rows, K, w->base, w->base + align256(qsb), s);
+  e = qm::launch_repack(type, src, rows, K, kraw, w->base, w->base + align256(qsb), s);
   if (e == hipSuccess && staged) e = hipStreamSynchronize(s);
   if (staged) (void)hipFree(staged);
   if (e != hipSuccess) {
@@ -374,11 +386,15 @@ int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* 
   return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_gemv_blocksums");
 }
 
-// qmatmul_gemm, qmatmul_gemm_ex and qmatmul_gemm_noalloc: one argument check and dispatch. act32 = 0 takes per-256
-// activation scales (asc [K/256][M_stride]); the kernels then read the scale of 32-block b at row b >> 3.
+// qmatmul_gemm, qmatmul_gemm_ex, qmatmul_gemm_ws and qmatmul_gemm_noalloc: one argument check and dispatch. act32 = 0
+// takes per-256 activation scales (asc [K/256][M_stride]); the kernels then read the scale of 32-block b at row b >> 3.
+// The workspace of the f16 path comes from the per-device pool (WS_POOL), the caller (WS_CALLER: ws, ws_bytes) or the
+// static scratch array (WS_STATIC); every other case needs none.
+enum WsMode { WS_POOL, WS_CALLER, WS_STATIC };
+
 static int gemm_impl(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
-                     int M, int M_stride, int act32, float* C, int ldc, int c_off, int accumulate, bool noalloc,
-                     void* stream) {
+                     int M, int M_stride, int act32, float* C, int ldc, int c_off, int accumulate, WsMode wm,
+                     void* ws, size_t ws_bytes, void* stream) {
   if (int st = check_acts(fn, w, aq, asc, absum, M, M_stride)) return st;
   if (!C) return fail(QM_ERR_ARG, "%s: null output", fn);
   if (w->rows % 16) return fail(QM_ERR_SHAPE, "%s: rows %d not a multiple of 16", fn, w->rows);
@@ -404,37 +420,55 @@ static int gemm_impl(const char* fn, const qm_weight* w, const int8_t* aq, const
   hipError_t e;
   if (qm::f16_gemm_supported(w->type, M, w->view.K)) {
     void* scr = nullptr;  // null: the f16 path takes its workspace from the per-device pool
-    if (noalloc) {
+    const size_t need = qm::f16_workspace_bytes(M, w->view.K);
+    if (wm == WS_STATIC) {
       size_t cap = 0;
       e = qm::f16_scratch(&scr, &cap);
       if (e != hipSuccess) return hip_fail(e, "qmatmul_gemm_noalloc: scratch lookup");
-      const size_t need = qm::f16_workspace_bytes(M, w->view.K);
       if (need > cap)
         return fail(QM_ERR_WORKSPACE, "%s: M %d x K %d needs %zu bytes of scratch, the static scratch holds %zu "
-                    "(use qmatmul_gemm)", fn, M, w->view.K, need, cap);
+                    "(use qmatmul_gemm or qmatmul_gemm_ws)", fn, M, w->view.K, need, cap);
+    } else if (wm == WS_CALLER) {
+      if (!ws || ws_bytes < need)
+        return fail(QM_ERR_WORKSPACE, "%s: M %d x K %d needs a workspace of %zu bytes (given %zu%s)", fn, M,
+                    w->view.K, need, ws_bytes, ws ? "" : ", null");
+      if (!aligned(ws, 256)) return fail(QM_ERR_ARG, "%s: the workspace must be 256-byte aligned", fn);
+      scr = ws;
     }
     e = qm::launch_gemm_f16(w->type, a, scr, (hipStream_t)stream);
   } else {
-    e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);  // (this kernel uses no scratch)
+    e = qm::launch_gemm(w->type, qm::GEMM_DENSE, a, (hipStream_t)stream);  // (this kernel uses no workspace)
   }
   return e == hipSuccess ? QM_OK : hip_fail(e, fn);
 }
 
 int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                  float* C, int ldc, int c_off, int accumulate, void* stream) {
-  return gemm_impl("qmatmul_gemm", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, false, stream);
+  return gemm_impl("qmatmul_gemm", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, WS_POOL, nullptr, 0,
+                   stream);
 }
 
 int qmatmul_gemm_ex(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                     int act32, float* C, int ldc, int c_off, int accumulate, void* stream) {
-  return gemm_impl("qmatmul_gemm_ex", w, aq, asc, absum, M, M_stride, act32, C, ldc, c_off, accumulate, false,
-                   stream);
+  return gemm_impl("qmatmul_gemm_ex", w, aq, asc, absum, M, M_stride, act32, C, ldc, c_off, accumulate, WS_POOL,
+                   nullptr, 0, stream);
+}
+
+size_t qmatmul_gemm_workspace_size(const qm_weight* w, int M) {
+  if (!w || M < 1) return 0;
+  return qm::f16_gemm_supported(w->type, M, w->view.K) ? qm::f16_workspace_bytes(M, w->view.K) : 0;
+}
+
+int qmatmul_gemm_ws(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                    int act32, float* C, int ldc, int c_off, int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  return gemm_impl("qmatmul_gemm_ws", w, aq, asc, absum, M, M_stride, act32, C, ldc, c_off, accumulate, WS_CALLER, ws,
+                   ws_bytes, stream);
 }
 
 int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
                          int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream) {
-  return gemm_impl("qmatmul_gemm_noalloc", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, true,
-                   stream);
+  return gemm_impl("qmatmul_gemm_noalloc", w, aq, asc, absum, M, M_stride, 1, C, ldc, c_off, accumulate, WS_STATIC,
+                   nullptr, 0, stream);
 }
 
 int qmatmul_gemm_blocksums(const qm_weight* w, const int8_t* aq, int M, int M_stride, int32_t* isum, void* stream) {
@@ -511,8 +545,12 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
                   "reference's expert GEMMs (zero/engine_moe.h:284-301)");
   if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)
     return fail(QM_ERR_SHAPE, "qmatmul_moe_grouped: NE %d, NU %d, T %d, M_stride %d, ldl %d", NE, NU, T, M_stride, ldl);
-  const int E = gate->K, F = down->K;
-  if (gate->rows != NE * F || up->rows != NE * F || up->K != E || down->rows != NE * E || F % 32 || E % 4)
+  // F: the down projection's K (the h row length); Fv: the experts' gate/up rows. Fv < F when the down projection's
+  // rows were padded with zero blocks at preparation (Q8_0 / Q4_0 / IQ4_NL experts of a width that is not whole
+  // superblocks: Flash Next's 640 as 768, zero/engine_moe.h:12, 318-326); h[Fv..F) is then zero.
+  const int E = gate->K, F = down->K, Fv = gate->rows / NE;
+  if (gate->rows != NE * Fv || up->rows != NE * Fv || up->K != E || down->rows != NE * E || Fv % 32 || E % 4 ||
+      !(Fv == F || (F % 256 == 0 && padded_k(Fv) == F)))
     return fail(QM_ERR_SHAPE,
                 "qmatmul_moe_grouped: gate %dx%d, up %dx%d, down %dx%d do not fit NE %d experts of F x E / E x F",
                 gate->rows, gate->K, up->rows, up->K, down->rows, down->K, NE);
@@ -547,7 +585,7 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
   // decode sizes: GEMV-shaped expert kernels (no tiles, no scatter): routing with gate/up, then down + combine
   if (T * NU <= 64 && NU <= 8 && F <= 4096 && E <= 8192) {
     const hipError_t e = qm::launch_moe_decode(gate->type, up->type, down->type, gate->view, up->view, down->view, T,
-                                               NU, E, F, logits, ldl, NE, escale, ids, wts, aq, asc, M_stride, hf, x,
+                                               NU, E, F, Fv, logits, ldl, NE, escale, ids, wts, aq, asc, M_stride, hf, x,
                                                accumulate, shd, s);
     return e == hipSuccess ? QM_OK : hip_fail(e, "qmatmul_moe_grouped");
   }
@@ -574,7 +612,7 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
     a.hsc = hsc;
     a.slots = L.slots;
     a.max_tiles = L.max_tiles;
-    a.expert_rows = F;
+    a.expert_rows = Fv;
     a.C = hf;
     a.ldc = F;
     if (fused) {
@@ -585,6 +623,9 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
       if (e == hipSuccess) e = qm::launch_gemm(up->type, qm::GEMM_MOE_UH, a, s);
     }
   }
+  // (padded h columns: scale 0 -- their weight blocks are zero, so the products are 0 whatever the int8 values)
+  if (e == hipSuccess && Fv < F) e = qm::launch_fill_i32((int*)(hsc + (size_t)(Fv / 32) * L.slots), 0,
+                                                         (size_t)((F - Fv) / 32) * L.slots, s);
   if (e == hipSuccess) {
     qm::GemmArgs a{};
     a.w = down->view;

@@ -218,7 +218,7 @@ __device__ __forceinline__ void moe_store(const GemmArgs& a, int slot, int n, bo
     const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
     const int q = (int)__builtin_rintf(h * inv);
     if (ok) {
-      a.hq[(size_t)slot * a.expert_rows + n] = (int8_t)q;
+      a.hq[(size_t)slot * a.ldc + n] = (int8_t)q;
       if (lc == 0) a.hsc[(size_t)(n / 32) * a.slots + slot] = amax / 127.0f;
     }
   }

@@ -206,6 +206,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   };
 
   f32x16 tq[4], res[4];
+  float sv256[4];  // S256: the superblock's activation scale of each token tile
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -296,6 +297,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (S256 && !DUMP) {
+        // the superblock's scale (its last pair's stage) is read before this pair's barrier: the next superblock's
+        // first pair overwrites that stage after the barrier, possibly while a slower wave is still in this epilogue
+        if (p == 3)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) sv256[t] = sasc[cur][0][32 * t + lc];
+      }
       store(cur ^ 1);
       store_sa(cur ^ 1);
 #pragma unroll
@@ -334,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         const uint4 uv = *(const uint4*)(a.u + (size_t)(m0 + 32 * t + lc) * nb + 8 * s + 4 * h);
         const f32x16 tmn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mnop, __builtin_bit_cast(bf16x8, uv), zero16, 0, 0, 0);
         if constexpr (S256) {
-          const float sv = sasc[(4 * s + 3) & 1][0][32 * t + lc];  // (the superblock's scale: its last pair's stage)
+          const float sv = sv256[t];
 #pragma unroll
           for (int r = 0; r < 16; ++r) res[t][r] = fmaf(dr[r] * sv, tq[t][r], fmaf(dmr[r], tmn[r], res[t][r]));
         } else {
@@ -386,11 +394,13 @@ bool f16_gemm_supported(int type, int M, int K) {
 // One memory pool per device for the per-call workspace (stream-ordered: concurrent calls on different streams get
 // different buffers; the pool keeps freed memory for the next call).
 static hipError_t f16_pool(hipMemPool_t* out) {
+  static std::mutex mu;
   static hipMemPool_t pools[64] = {};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
   if (!pools[dev]) {
     hipMemPoolProps props{};
     props.allocType = hipMemAllocationTypePinned;

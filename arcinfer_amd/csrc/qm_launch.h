@@ -9,7 +9,10 @@
 namespace qm {
 
 // GGUF rows -> prepared planes (qm_prep.hip)
-hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t* qs, uint8_t* hdr, hipStream_t s);
+// K: the prepared row length (a multiple of 256); kraw: 32-blocks per raw row (K / 32, or fewer for a padded
+// Q8_0 / Q4_0 / IQ4_NL row)
+hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, int kraw, uint8_t* qs, uint8_t* hdr,
+                         hipStream_t s);
 // f32 rows -> int8 + per-32 scales + per-16 sums (qm_prep.hip)
 hipError_t launch_quantize(const float* x, int ldx, int M, int M_stride, int K, bool act32, int8_t* aq, float* asc,
                            int16_t* absum, hipStream_t s);
@@ -43,11 +46,11 @@ struct GemmArgs {
   const int* tiles;    // [0] = count, then (expert, first slot, rows) per tile
   const int* rowmap;   // slot -> token (gate/up), or null (down: slot rows)
   const float* rowscale;  // slot -> routing weight (down), or null
-  int8_t* hq;          // gate/up: quantized h rows [slots][F]
+  int8_t* hq;          // gate/up: quantized h rows [slots][ldc] (ldc = F, the down projection's K)
   float* hsc;          // gate/up: h scales [F/32][slots]
   int slots;           // row stride of hsc
   int max_tiles;
-  int expert_rows;     // rows per expert in w (F for gate/up, E for down)
+  int expert_rows;     // rows per expert in w (Fv <= F for gate/up, E for down)
 };
 // MoE tile modes: GATEUP (gate and up of one type in one launch: h quantized), G (gate alone: f32 g into C),
 // UH (up alone after G: h from u and g, quantized), DOWN (routing-weighted y)
@@ -103,8 +106,8 @@ hipError_t launch_fill_i32(int* p, int value, size_t n, hipStream_t s);
 // MoE at decode sizes (qm_moe_dec.hip): routing + gate/up -> ids, wts, h (f32 [T*NU][F]), then down + combine into x
 // (gate, up, down of types tg, tu, td; escale: routing expert scales or null; sh: the shared expert or sh.sh null)
 hipError_t launch_moe_decode(int tg, int tu, int td, const WView& gate, const WView& up, const WView& down, int T,
-                             int NU, int E, int F, const float* logits, int ldl, int NE, const float* escale, int* ids,
-                             float* wts, const int8_t* aq, const float* asc, int M_stride, float* h, float* x,
+                             int NU, int E, int F, int Fv, const float* logits, int ldl, int NE, const float* escale,
+                             int* ids, float* wts, const int8_t* aq, const float* asc, int M_stride, float* h, float* x,
                              int accumulate, const MoeShared& sh, hipStream_t s);
 
 }  // namespace qm

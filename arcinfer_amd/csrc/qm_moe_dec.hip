@@ -35,7 +35,9 @@ __device__ __forceinline__ int sum16(uint4 v) {
 
 }  // namespace
 
-// Gate/up: grid (T * NU slots, ceil(F / rows per work-group)). The work-group stages its token's int8 row in LDS as two
+// Gate/up: grid (T * NU slots, ceil(F / rows per work-group)); h rows of F values, of which the first Fv are the
+// experts' rows (Fv < F: the down projection's rows were padded with zero blocks to F = Fv rounded up to 256, and
+// h[Fv..F) is written as 0). The work-group stages its token's int8 row in LDS as two
 // 16-byte planes, with the per-32 scales and per-16 sums; with routing inside (logits non-null, T <= 4) wave 0 routes
 // the token while the others stage. Each LPR-lane group computes one expert row j: GU_BOTH h = u * silu(g) from gate
 // and up, GU_GATE stores g into h, GU_UP reads g from h and stores u * silu(g).
@@ -43,7 +45,7 @@ template <int TYPE, int MODE, int CH, int PER_LANE, int LPR = 32>
 __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView up, const float* __restrict__ logits,
                                                              int ldl, int NE, int* __restrict__ ids,
                                                              float* __restrict__ wts, const float* __restrict__ escale,
-                                                             int NU, int F, const int8_t* __restrict__ aq,
+                                                             int NU, int F, int Fv, const int8_t* __restrict__ aq,
                                                              const float* __restrict__ asc, int M_stride,
                                                              float* __restrict__ h) {
   extern __shared__ uint4 smem[];
@@ -82,8 +84,8 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
   const int e = sel[k];
   constexpr int RPW = 256 / LPR;  // expert rows per work-group
   const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
-  const int j = min((int)blockIdx.y * RPW + grp, F - 1);
-  const size_t row = (size_t)e * F + j;
+  const int jj = (int)blockIdx.y * RPW + grp, j = min(jj, Fv - 1);
+  const size_t row = (size_t)e * Fv + j;
   RawBlk r0[CH], r1[MODE == GU_BOTH ? CH : 1];
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
@@ -105,9 +107,11 @@ __global__ __launch_bounds__(256) void moe_gateup_dec_kernel(WView gate, WView u
   }
   v0 = wave_sum_width(v0, LPR);
   if constexpr (MODE == GU_BOTH) v1 = wave_sum_width(v1, LPR);
-  if (gl == 0 && (int)blockIdx.y * RPW + grp < F) {
-    float* hp = h + (size_t)slot * F + j;
-    if constexpr (MODE == GU_BOTH) {
+  if (gl == 0 && jj < F) {
+    float* hp = h + (size_t)slot * F + jj;
+    if (jj >= Fv) {
+      *hp = 0.0f;
+    } else if constexpr (MODE == GU_BOTH) {
       *hp = v1 * (v0 / (1.0f + expf(-v0)));
     } else if constexpr (MODE == GU_GATE) {
       *hp = v0;
@@ -217,14 +221,14 @@ __global__ __launch_bounds__(256) void moe_down_dec_kernel(WView down, int E, co
 
 template <int TYPE, int MODE, int PL>
 static void gateup_dec(int slots, size_t shg, int nbE, const WView& gate, const WView& up, const float* logits,
-                       int ldl, int NE, int* ids, float* wts, const float* escale, int NU, int F, const int8_t* aq,
-                       const float* asc, int M_stride, float* h, hipStream_t s) {
+                       int ldl, int NE, int* ids, float* wts, const float* escale, int NU, int F, int Fv,
+                       const int8_t* aq, const float* asc, int M_stride, float* h, hipStream_t s) {
   // 16 lanes per expert row up to 64 blocks per row (16 rows per work-group: half the work-groups, each routing and
   // staging the token once; measured faster at 4 and 8 tokens, equal at 1), 32 lanes beyond
 #define QM_GUD(CH, LPR)                                                                                       \
   moe_gateup_dec_kernel<TYPE, MODE, CH, PL, LPR>                                                              \
       <<<dim3((unsigned)slots, (unsigned)((F + 256 / LPR - 1) / (256 / LPR))), 256, shg, s>>>(                \
-          gate, up, logits, ldl, NE, ids, wts, escale, NU, F, aq, asc, M_stride, h)
+          gate, up, logits, ldl, NE, ids, wts, escale, NU, F, Fv, aq, asc, M_stride, h)
   if (nbE <= 16) QM_GUD(1, 16);
   else if (nbE <= 32) QM_GUD(2, 16);
   else if (nbE <= 64) QM_GUD(4, 16);
@@ -234,13 +238,13 @@ static void gateup_dec(int slots, size_t shg, int nbE, const WView& gate, const 
 }
 
 template <int TYPE, int MODE>
-static hipError_t gateup_typed(int T, int NU, int E, int F, const WView& gate, const WView& up, const float* logits,
+static hipError_t gateup_typed(int T, int NU, int E, int F, int Fv, const WView& gate, const WView& up, const float* logits,
                                int ldl, int NE, int* ids, float* wts, const float* escale, const int8_t* aq,
                                const float* asc, int M_stride, float* h, hipStream_t s) {
   const int slots = T * NU, nbE = E / 32;
   const size_t shg = (size_t)E + sizeof(float) * nbE + sizeof(int) * nbE;
-  if (NE <= 256) gateup_dec<TYPE, MODE, 4>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, escale, NU, F, aq, asc, M_stride, h, s);
-  else gateup_dec<TYPE, MODE, 16>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, escale, NU, F, aq, asc, M_stride, h, s);
+  if (NE <= 256) gateup_dec<TYPE, MODE, 4>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, escale, NU, F, Fv, aq, asc, M_stride, h, s);
+  else gateup_dec<TYPE, MODE, 16>(slots, shg, nbE, gate, up, logits, ldl, NE, ids, wts, escale, NU, F, Fv, aq, asc, M_stride, h, s);
   return hipGetLastError();
 }
 
@@ -267,12 +271,12 @@ static hipError_t down_typed(int T, int NU, int E, int F, const WView& down, con
   X(T_IQ3_XXS) X(T_Q6_K)
 
 template <int MODE>
-static hipError_t gateup_any(int type, int T, int NU, int E, int F, const WView& gate, const WView& up,
+static hipError_t gateup_any(int type, int T, int NU, int E, int F, int Fv, const WView& gate, const WView& up,
                              const float* logits, int ldl, int NE, int* ids, float* wts, const float* escale,
                              const int8_t* aq, const float* asc, int M_stride, float* h, hipStream_t s) {
   switch (type) {
 #define QM_CASE(TY) \
-  case TY: return gateup_typed<TY, MODE>(T, NU, E, F, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
+  case TY: return gateup_typed<TY, MODE>(T, NU, E, F, Fv, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
     QM_MOE_TYPES(QM_CASE)
 #undef QM_CASE
     default: return hipErrorInvalidValue;
@@ -280,7 +284,7 @@ static hipError_t gateup_any(int type, int T, int NU, int E, int F, const WView&
 }
 
 hipError_t launch_moe_decode(int tg, int tu, int td, const WView& gate, const WView& up, const WView& down, int T,
-                             int NU, int E, int F, const float* logits, int ldl, int NE, const float* escale, int* ids,
+                             int NU, int E, int F, int Fv, const float* logits, int ldl, int NE, const float* escale, int* ids,
                              float* wts, const int8_t* aq, const float* asc, int M_stride, float* h, float* x,
                              int accumulate, const MoeShared& sh, hipStream_t s) {
   if (T > 4 || tg != tu) {
@@ -292,11 +296,11 @@ hipError_t launch_moe_decode(int tg, int tu, int td, const WView& gate, const WV
   }
   hipError_t e;
   if (tg == tu) {
-    e = gateup_any<GU_BOTH>(tg, T, NU, E, F, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
+    e = gateup_any<GU_BOTH>(tg, T, NU, E, F, Fv, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
   } else {
-    e = gateup_any<GU_GATE>(tg, T, NU, E, F, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
+    e = gateup_any<GU_GATE>(tg, T, NU, E, F, Fv, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
     if (e == hipSuccess)
-      e = gateup_any<GU_UP>(tu, T, NU, E, F, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
+      e = gateup_any<GU_UP>(tu, T, NU, E, F, Fv, gate, up, logits, ldl, NE, ids, wts, escale, aq, asc, M_stride, h, s);
   }
   if (e != hipSuccess) return e;
   switch (td) {

@@ -6,8 +6,12 @@ namespace qm {
 // ---------------------------------------------------------------------------------------------------------------
 // One thread per (row, superblock): reads the GGUF superblock bytewise (any alignment) and writes its payload and
 // header into the two planes (layout in qm_device.h). Follows the field offsets of src/quants.h:89-315.
+// kraw: 32-blocks per raw row. It is K / 32 except for the types of 32-element blocks (Q8_0, Q4_0, IQ4_NL) whose rows
+// are not whole superblocks: those are padded to K = the next multiple of 256 with zero blocks (scale 0, so every
+// padded element decodes to 0), as the reference's pad_small_block_rows / load_w_pad do (src/quants.h:581-595;
+// zero/engine.h:2102-2116).
 template <int TYPE>
-__global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int rows, int K,
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int rows, int K, int kraw,
                                                      uint8_t* __restrict__ qs, uint8_t* __restrict__ hdr) {
   using Tr = Traits<TYPE>;
   const int nsb = K / 256;
@@ -15,15 +19,21 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
   if (i >= (long)rows * nsb) return;
   const long n = i / nsb;
   const int s = (int)(i % nsb);
-  const uint8_t* p = raw + ((size_t)n * nsb + s) * Tr::GGUF_SB;
+  // (the small-block types: raw rows of kraw blocks of Tr::GGUF_SB / 8 bytes; the others: rows of nsb superblocks)
+  constexpr bool small = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL;
+  const size_t row_bytes = small ? (size_t)kraw * (Tr::GGUF_SB / 8) : (size_t)nsb * Tr::GGUF_SB;
+  const uint8_t* p = raw + (size_t)n * row_bytes + (size_t)s * Tr::GGUF_SB;
+  const int nblk = min(8, kraw - 8 * s);  // blocks of this superblock present in the raw row
+  (void)nblk;
   uint8_t* q = qs + ((size_t)n * (K / 32) + (size_t)s * 8) * Tr::QB;
   uint8_t* h = hdr + ((size_t)n * nsb + s) * Tr::HB;
   if constexpr (TYPE == T_Q8_0) {
     // 8 GGUF blocks of (f16 d, int8 q[32])
     for (int b = 0; b < 8; ++b) {
-      h[2 * b] = p[34 * b];
-      h[2 * b + 1] = p[34 * b + 1];
-      for (int e = 0; e < 32; ++e) q[32 * b + e] = p[34 * b + 2 + e];
+      const bool in = b < nblk;
+      h[2 * b] = in ? p[34 * b] : 0;
+      h[2 * b + 1] = in ? p[34 * b + 1] : 0;
+      for (int e = 0; e < 32; ++e) q[32 * b + e] = in ? p[34 * b + 2 + e] : 0;
     }
   } else if constexpr (TYPE == T_Q4_K) {
     // d, dmin, scales[12] | qs[128]: chunk j (64 elements) = qs[32j..32j+31], low nibbles elements 0..31 of the
@@ -69,9 +79,10 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
   } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
     // 8 GGUF blocks of (f16 d, 16 nibble bytes)
     for (int b = 0; b < 8; ++b) {
-      h[2 * b] = p[18 * b];
-      h[2 * b + 1] = p[18 * b + 1];
-      for (int t = 0; t < 16; ++t) q[16 * b + t] = p[18 * b + 2 + t];
+      const bool in = b < nblk;
+      h[2 * b] = in ? p[18 * b] : 0;
+      h[2 * b + 1] = in ? p[18 * b + 1] : 0;
+      for (int t = 0; t < 16; ++t) q[16 * b + t] = in ? p[18 * b + 2 + t] : 0;
     }
   } else if constexpr (TYPE == T_Q6_K) {
     // ql[128] | qh[64] | scales[16] | d (src/quants.h:115-135): element 128n + 32c + l has its low 4 bits in
@@ -149,22 +160,23 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
   }
 }
 
-hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, uint8_t* qs, uint8_t* hdr, hipStream_t s) {
+hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, int kraw, uint8_t* qs, uint8_t* hdr,
+                         hipStream_t s) {
   const long n = (long)rows * (K / 256);
   const dim3 grid((unsigned)((n + 255) / 256)), block(256);
   switch (type) {
-    case T_Q8_0: repack_kernel<T_Q8_0><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_Q4_K: repack_kernel<T_Q4_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ4_NL: repack_kernel<T_IQ4_NL><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ2_XXS: repack_kernel<T_IQ2_XXS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ2_XS: repack_kernel<T_IQ2_XS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ2_S: repack_kernel<T_IQ2_S><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
-    case T_IQ3_XXS: repack_kernel<T_IQ3_XXS><<<grid, block, 0, s>>>(raw, rows, K, qs, hdr); break;
+    case T_Q8_0: repack_kernel<T_Q8_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q4_K: repack_kernel<T_Q4_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ4_NL: repack_kernel<T_IQ4_NL><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ2_XXS: repack_kernel<T_IQ2_XXS><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ2_XS: repack_kernel<T_IQ2_XS><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ2_S: repack_kernel<T_IQ2_S><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ3_XXS: repack_kernel<T_IQ3_XXS><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -18,10 +18,28 @@ SB_BYTES = {Q4_0: 144, Q8_0: 272, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 144, 
             IQ2_XS: 74, IQ3_XXS: 98, IQ2_S: 82}
 
 
+SMALL_BLOCK_TYPES = (Q8_0, Q4_0, IQ4_NL)  # 32-element blocks: rows may end inside a superblock
+
+
 def row_bytes(qtype, K):
+    if qtype in SMALL_BLOCK_TYPES and K % 32 == 0:
+        return K // 32 * (SB_BYTES[qtype] // 8)
     if K % 256:
         raise ValueError(f"K = {K} is not a multiple of 256")
     return K // 256 * SB_BYTES[qtype]
+
+
+def padded_k(K):
+    return (K + 255) // 256 * 256
+
+
+def pad_small_rows(qtype, W, K):
+    """Rows of K elements of a 32-element block type -> rows of padded_k(K) elements, the added blocks all zero (an
+    f16 zero scale: they decode to 0), as the reference's pad_small_block_rows (src/quants.h:581-595)."""
+    assert qtype in SMALL_BLOCK_TYPES and K % 32 == 0
+    out = np.zeros((W.shape[0], row_bytes(qtype, padded_k(K))), dtype=np.uint8)
+    out[:, :row_bytes(qtype, K)] = W
+    return out
 
 
 def weight_bytes(qtype, N, K):
@@ -57,7 +75,7 @@ def synth_weight(qtype, N, K, seed, sigma=None):
         blk[:, 0] = d & 0xFF
         blk[:, 1] = d >> 8
         blk[:, 2:] = rng.integers(-127, 128, size=(nblk, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
-        return blk.reshape(N, nsb * 272)
+        return blk.reshape(N, K // 32 * 34)
     if qtype in (Q4_0, IQ4_NL):
         sig = 0.02 if sigma is None else sigma
         nblk = N * K // 32
@@ -65,7 +83,7 @@ def synth_weight(qtype, N, K, seed, sigma=None):
         d = f16_bits(np.abs(rng.normal(0.0, sig, nblk)) / 8.0)
         blk[:, 0] = d & 0xFF
         blk[:, 1] = d >> 8
-        return blk.reshape(N, nsb * 144)
+        return blk.reshape(N, K // 32 * 18)
     sig = 0.01 if sigma is None else sigma
     sb = SB_BYTES[qtype]
     raw = rng.integers(0, 256, size=(N * nsb, sb), dtype=np.uint8)

@@ -32,6 +32,8 @@ SIGNATURES = [
     ("qmatmul_gemm", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_gemm_ex", _I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _P]),
     ("qmatmul_gemm_noalloc", _I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    ("qmatmul_gemm_workspace_size", _Z, [_P, _I]),
+    ("qmatmul_gemm_ws", _I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _I, _P, _Z, _P]),
     ("qmatmul_moe_workspace_size", _Z, [_I, _I, _I, _I, _I]),
     ("qmatmul_moe_route", _I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     ("qmatmul_moe_grouped", _I, [_P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _Z, _P]),
@@ -116,12 +118,15 @@ def _stream(stream):
 
 
 class QWeight:
-    """A prepared weight (qm_weight*) from GGUF bytes: a uint8 tensor (device or CPU) or a numpy array."""
+    """A prepared weight (qm_weight*) from GGUF bytes: a uint8 tensor (device or CPU) or a numpy array. K is the raw
+    row length; Q8_0 / Q4_0 / IQ4_NL rows of K % 256 != 0 are padded with zero blocks, and self.K is then the
+    prepared (padded) length, self.K_raw the given one."""
 
     def __init__(self, qtype, raw, rows, K, stream=None):
         import numpy as np
         import torch
         self.qtype, self.rows, self.K = int(qtype), int(rows), int(K)
+        self.K_raw = self.K
         h = ctypes.c_void_p()
         if isinstance(raw, np.ndarray):
             raw = np.ascontiguousarray(raw)
@@ -132,6 +137,9 @@ class QWeight:
             _call("qmatmul_prepare_weight", self.qtype, _ptr(raw), 1 if raw.is_cuda else 0, self.rows, self.K,
                   _stream(stream), ctypes.byref(h))
         self.handle = h
+        k = ctypes.c_int()
+        _call("qmatmul_weight_info", h, None, None, ctypes.byref(k))
+        self.K = k.value
 
     @property
     def nbytes(self):
@@ -193,6 +201,25 @@ def gemm(w, aq, asc, absum, M=None, C=None, ldc=None, c_off=0, accumulate=0, str
         return C
     _call("qmatmul_gemm_noalloc" if noalloc else "qmatmul_gemm", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, _ptr(C),
           w.rows if ldc is None else ldc, c_off, accumulate, _stream(stream))
+    return C
+
+
+def gemm_workspace_size(w, M):
+    return load_library().qmatmul_gemm_workspace_size(w.handle, M)
+
+
+def gemm_ws(w, aq, asc, absum, ws, M=None, C=None, ldc=None, c_off=0, accumulate=0, stream=None, act32=True):
+    """qmatmul_gemm_ws: the prompt GEMM with a caller-owned workspace ws (a uint8 device tensor, or None when
+    gemm_workspace_size(w, M) is 0)."""
+    import torch
+    Ms = aq.shape[0]
+    M = Ms if M is None else M
+    if C is None:
+        C = torch.empty((M, w.rows), dtype=torch.float32, device=aq.device)
+        ldc = w.rows
+    _call("qmatmul_gemm_ws", w.handle, _ptr(aq), _ptr(asc), _ptr(absum), M, Ms, int(act32), _ptr(C),
+          w.rows if ldc is None else ldc, c_off, accumulate, _ptr(ws), 0 if ws is None else ws.numel(),
+          _stream(stream))
     return C
 
 

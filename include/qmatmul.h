@@ -18,6 +18,13 @@
  *
  * Weights: GGUF blocks, rows of K elements, K a multiple of 256 (Q8_0: 8 blocks of 32 per 256). A weight is
  * prepared once (qmatmul_prepare_weight) into this library's own device layout and then read by every product.
+ * Rows of the 32-element block types (Q8_0, Q4_0, IQ4_NL) may have any K % 32 == 0: they are padded at preparation
+ * with zero blocks to the next multiple of 256, which is then the weight's K (qmatmul_weight_info); the activations
+ * of such a weight are K values long, the padding zeros.
+ *
+ * Output buffers (C, x) must be ordinary device memory (hipMalloc, a torch tensor): when a prompt GEMM has few output
+ * tiles, its two K halves are added into C with hardware float atomics, which fine-grained or host-coherent memory
+ * does not guarantee.
  *
  * accumulate (all products): 0 = store, 1 = C += result, 2 = C = silu(C) * result (GEMM only, fused SwiGLU:
  * C holds the gate projection), as zero/kernels/gemm.cl:464-471.
@@ -62,20 +69,22 @@ const char* qmatmul_last_error(void);
 size_t qmatmul_sb_bytes(int type);
 
 /* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S, Q6_K,
- * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock). */
+ * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock; a padded Q8_0 / Q4_0 / IQ4_NL row counts its zero blocks). */
 size_t qmatmul_weight_bytes(int type, int rows, int K);
 
 /* Prepares a weight from its GGUF bytes: rows x (K/256) superblocks, row-major, as stored in a GGUF tensor (a
  * stacked expert tensor [NE][N][K] is NE*N rows). raw is a device pointer if raw_on_device, else a host pointer.
  * Allocates the prepared copy and returns it in *out. Replaces Engine::make_weight / upload_padded
- * (zero/engine.h:1936-2014; src/quants.h:643-681). */
+ * (zero/engine.h:1936-2014; src/quants.h:643-681). Q8_0, Q4_0 and IQ4_NL rows may be K % 32 == 0 long (rows of
+ * K/32 GGUF blocks): they are padded with zero blocks to K rounded up to 256, as the reference's load_w_pad /
+ * pad_small_block_rows (zero/engine.h:2102-2116; src/quants.h:581-595); every other type needs K % 256 == 0. */
 int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int rows, int K, void* stream,
                            qm_weight** out);
 
 /* Frees a prepared weight (waits for the device). */
 int qmatmul_release_weight(qm_weight* w);
 
-/* Type, rows and K of a prepared weight (any output pointer may be NULL). */
+/* Type, rows and K of a prepared weight (any output pointer may be NULL); K is the prepared (padded) row length. */
 int qmatmul_weight_info(const qm_weight* w, int* type, int* rows, int* K);
 
 /* Activation quantizer: x f32 [M][ldx] -> aq, asc, absum (layout above; rows M..M_stride-1 zeroed).
@@ -132,7 +141,8 @@ int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const i
  * gemm_ext (zero/engine.h:3234-3297; zero/kernels/gemm.cl:132-475). Q4_K is computed exactly (scales and mins),
  * not requantized as the reference's W8 path does (zero/kernels/decode.cl:455-507). Q4_K with M >= 128 runs on the
  * f16 matrix pipe (exact integer block sums from f16 products) and takes a per-call workspace of about 2*M*K bytes
- * from a per-device stream-ordered memory pool; every other case runs on int8 MFMA and allocates nothing. */
+ * from a per-device stream-ordered memory pool; every other case runs on int8 MFMA and allocates nothing. A caller
+ * that owns all memory passes the workspace itself (qmatmul_gemm_ws). */
 int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                  float* C, int ldc, int c_off, int accumulate, void* stream);
 /* qmatmul_gemm with the act32 argument of Engine::matmul / matmul1 (zero/engine.h:3151, 3184, 3247; gemm.cl built
@@ -143,17 +153,29 @@ int qmatmul_gemm(const qm_weight* w, const int8_t* aq, const float* asc, const i
 int qmatmul_gemm_ex(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
                     int act32, float* C, int ldc, int c_off, int accumulate, void* stream);
 
+/* The prompt GEMM with a caller-owned workspace, as the reference's engine owns its W8 staging buffers
+ * (zero/engine.h:3238-3246): qmatmul_gemm_ex's arguments plus ws (device, 256-byte aligned) of at least
+ * qmatmul_gemm_workspace_size(w, M) bytes. That size is 0 for every call but Q4_K with M >= 128 (then
+ * 2*Mp*K + 4*Mp*K/32 bytes, Mp = M rounded up to 128); ws may be NULL when it is 0. No allocation, no host
+ * synchronisation; calls on different streams need different workspaces. QM_ERR_WORKSPACE if ws is too small. */
+size_t qmatmul_gemm_workspace_size(const qm_weight* w, int M);
+int qmatmul_gemm_ws(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M, int M_stride,
+                    int act32, float* C, int ldc, int c_off, int accumulate, void* ws, size_t ws_bytes, void* stream);
+
 /* qmatmul_gemm without any device allocation. No counterpart in the reference: for callers that cannot allocate
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same arguments, results and kernels
  * as qmatmul_gemm; where qmatmul_gemm would take its pool workspace, this entry uses a static 32 MiB device array
  * (one per GPU, held until the process ends) and returns QM_ERR_WORKSPACE when the call needs more
  * (f16 path: 2*Mp*K + 4*Mp*K/32 bytes, Mp = M rounded up to 128; e.g. M 2048 x K 5120 needs 22.3 MB).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different streams, or threads) race
- * and must be ordered by the caller. Each call writes every scratch byte it reads before reading it. */
+ * and must be ordered by the caller. Each call writes every scratch byte it reads before reading it. It takes per-32
+ * activation scales only (qmatmul_gemm's act32 = 1); a caller with per-256 scales that cannot allocate passes its
+ * own workspace to qmatmul_gemm_ws. */
 int qmatmul_gemm_noalloc(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M,
                          int M_stride, float* C, int ldc, int c_off, int accumulate, void* stream);
 
-/* Workspace bytes of qmatmul_moe_grouped for T tokens, NE experts, NU experts per token, hidden E, expert width F. */
+/* Workspace bytes of qmatmul_moe_grouped for T tokens, NE experts, NU experts per token, hidden E, expert width F
+ * (the down projection's K). */
 size_t qmatmul_moe_workspace_size(int T, int NE, int NU, int E, int F);
 
 /* Routing alone (test and reuse): top NU of each token's NE logits (row stride ldl; ties go to the lower expert),
@@ -165,7 +187,9 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
 /* Mixture-of-experts FFN over T tokens (Qwen3.5-MoE style), the expert part of Engine::layer_moe
  * (zero/engine_moe.h:8-282):
  *   x[t][:E] (op)= sum_k w_tk * down_e( q( silu(gate_e(a_t)) * up_e(a_t) ) ),  e = k-th expert of token t
- * gate, up: NE*F rows of E; down: NE*E rows of F (stacked experts). a_t: token t of aq/asc (E values). q(): the h
+ * gate, up: NE*Fv rows of E; down: NE*E rows of F (stacked experts), F = Fv, or F = Fv rounded up to 256 for a down
+ * projection prepared from Fv-long Q8_0 / Q4_0 / IQ4_NL rows (zero-padded; the h rows then have F values, the last
+ * F - Fv zero: Flash Next's 640-wide experts as 768, zero/engine_moe.h:12, 318-326). a_t: token t of aq/asc (E values). q(): the h
  * rows quantized per 32 as moe_quant (moe.cl:251-282). Route, exclusive scan into tiles, device-side scatter of
  * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
  * order (moe.cl:332-340); at decode sizes (T * NU <= 64) GEMV-shaped expert kernels instead. Gate, up and down each

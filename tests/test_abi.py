@@ -36,6 +36,11 @@ def test_host_only_entry_points(qm):
     assert lib.qmatmul_sb_bytes(21) == 110 and lib.qmatmul_sb_bytes(23) == 136 and lib.qmatmul_sb_bytes(6) == 0 and lib.qmatmul_sb_bytes(2) == 144
     assert lib.qmatmul_weight_bytes(23, 17408, 5120) >= 17408 * 20 * 136
     assert lib.qmatmul_weight_bytes(23, 16, 100) == 0
+    # 32-element block types: rows of K % 32 == 0 are padded to whole superblocks (640 -> 768); others refuse them
+    assert lib.qmatmul_weight_bytes(8, 16, 640) == lib.qmatmul_weight_bytes(8, 16, 768)
+    assert lib.qmatmul_weight_bytes(20, 16, 640) == lib.qmatmul_weight_bytes(20, 16, 768) > 0
+    assert lib.qmatmul_weight_bytes(23, 16, 640) == 0 and lib.qmatmul_weight_bytes(8, 16, 648) == 0
+    assert lib.qmatmul_gemm_workspace_size(None, 128) == 0
     assert lib.qmatmul_moe_workspace_size(4096, 256, 8, 2048, 512) > 32768 * 2048 * 4
     L = qm.moe_ws_layout(4096, 256, 8, 2048, 512)
     assert L.slots == 32768 and L.max_tiles == 32768 // L.tile_rows + 2 * 256 and L.total >= L.y + 32768 * 2048 * 4
@@ -50,6 +55,8 @@ def test_argument_errors_need_no_gpu(qm):
     buf = (ctypes.c_uint8 * 16)()
     assert lib.qmatmul_prepare_weight(6, buf, 0, 16, 256, None, ctypes.byref(h)) == 3
     assert lib.qmatmul_prepare_weight(23, buf, 0, 16, 100, None, ctypes.byref(h)) == 2
+    assert lib.qmatmul_prepare_weight(23, buf, 0, 16, 640, None, ctypes.byref(h)) == 2  # (IQ4_XS: whole superblocks)
+    assert lib.qmatmul_gemm_ws(None, None, None, None, 1, 1, 1, None, 0, 0, 0, None, 0, None) == 1
     assert lib.qmatmul_gemv(None, None, None, None, 1, 1, None, 0, 0, 0, None) == 1
     assert lib.qmatmul_quantize_act(buf, 32, 1, 1, 33, buf, buf, buf, None) == 2
     # per-256 activation scales (act32 = 0) need K % 256 == 0; act32 is 0 or 1

@@ -152,6 +152,7 @@ def test_gemv_baseline_q8_0_4096(qm, dev):
     torch.cuda.synchronize()
     ref = oracle.blockdot(F.Q8_0, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=1)
     assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+    assert_elementwise(C.cpu().numpy(), ref)
 
 
 @pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
@@ -241,7 +242,9 @@ def test_gemm_accumulate_modes(qm, dev, qtype):
 
 
 def test_gemm_baseline_q4_k_2k_sampled(qm, dev):
-    """BASELINE config 2 at full size: M 2048, K 5120, N 17408; every 64th output column against the oracle."""
+    """BASELINE config 2 at full size: M 2048, K 5120, N 17408. Every 67th output column against the oracle (67 is
+    coprime with the 128-row weight tile, so the 260 sampled columns cover every row position of the tile: every
+    wave, lane half and result register of the f16 epilogue), plus the whole last 128-row tile (rows 17280-17407)."""
     import torch
     M, N, K = 2048, 17408, 5120
     W = F.synth_weight(F.Q4_K, N, K, seed=2)
@@ -251,9 +254,14 @@ def test_gemm_baseline_q4_k_2k_sampled(qm, dev):
     C = qm.gemm(w, aq, asc, absum)
     torch.cuda.synchronize()
     Cn = C.cpu().numpy()
-    ref = oracle.blockdot(F.Q4_K, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), col_stride=64)
-    assert rel_err(Cn[:, ::64], ref[:, ::64]) < TOL_INT8_PATH
-    assert_elementwise(Cn[:, ::64], ref[:, ::64])
+    naq, nasc, nabs = aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy()
+    ref = oracle.blockdot(F.Q4_K, W, K, naq, nasc, nabs, col_stride=67)
+    assert len(set(np.arange(0, N, 67) % 128)) == 128
+    assert rel_err(Cn[:, ::67], ref[:, ::67]) < TOL_INT8_PATH
+    assert_elementwise(Cn[:, ::67], ref[:, ::67])
+    last = oracle.blockdot(F.Q4_K, W[N - 128:], K, naq, nasc, nabs)
+    assert rel_err(Cn[:, N - 128:], last) < TOL_INT8_PATH
+    assert_elementwise(Cn[:, N - 128:], last)
     assert np.all(np.isfinite(Cn))
 
 
@@ -286,6 +294,7 @@ def test_iq3_s_baseline_5120(qm, dev, M):
     ref = oracle.blockdot(F.IQ3_S, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=M,
                           col_stride=stride)
     assert rel_err(C.cpu().numpy()[:, ::stride], ref[:, ::stride]) < TOL_INT8_PATH
+    assert_elementwise(C.cpu().numpy()[:M, ::stride], ref[:, ::stride])
 
 
 @pytest.mark.parametrize("M,N,K,c_off,extra", [(300, 144, 1024, 3, 5), (64, 128, 256, 0, 0), (257, 272, 2048, 1, 2)])
