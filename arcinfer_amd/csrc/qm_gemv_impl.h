@@ -135,12 +135,24 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   const int grp = threadIdx.x / LPR, gl = threadIdx.x % LPR;
   const int G = gridDim.x * GPW;
   const int g0 = blockIdx.x * GPW + grp;
-  // steps: the group's rows; with two waves per row every group of the work-group runs the same number of steps
-  // (the combine's barrier), the extra steps of the shorter groups recomputing the last row without storing it
-  const int steps = WPR == 1 ? (g0 < rows ? (rows - 1 - g0) / G + 1 : 0) : (rows - 1 - (int)blockIdx.x * GPW) / G + 1;
+  // Rows: steps i < s2 sweep all groups in lockstep (row g0 + G i). With a split (a.split > 0: the work-groups of the
+  // first dispatch round, one per CU), s2 is two steps short of the sweep and the first-round groups then take the
+  // remaining rows: the second work-group on a CU issues its loads behind the first one's, so its rows arrive about
+  // two row steps later; on the 17408-wide down projection the two rounds then end together (12.4 vs 13.0 us in a
+  // launch loop on one box).
+  const int split = a.split, G1 = split * GPW;
+  const int s2 = split > 0 ? max(1, (rows + G - 1) / G - 2) : (rows + G - 1) / G;
+  auto row_of = [&](int i) { return i < s2 ? g0 + G * i : G * s2 + g0 + G1 * (i - s2); };
+  auto steps_of = [&](int g) {
+    if (split > 0 && g < G1 && G * s2 + g < rows) return s2 + (rows - 1 - G * s2 - g) / G1 + 1;
+    return g < rows ? min(s2, (rows - 1 - g) / G + 1) : 0;
+  };
+  // (with several waves per row every group of the work-group runs its first group's step count, for the combine's
+  // barrier; the extra steps of its other groups recompute a row past the end without storing it)
+  const int steps = WPR == 1 ? steps_of(g0) : steps_of((int)blockIdx.x * GPW);
   RawBlk cur[CH];
   auto fetch = [&](int i, RawBlk* dst) {
-    const int n = min(g0 + G * i, rows - 1);
+    const int n = min(row_of(i), rows - 1);
     const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
     const uint8_t* hrow = a.w.hdr + (size_t)n * (nb / 8) * Tr::HB;
 #pragma unroll
@@ -244,7 +256,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
           }
           block_dot<TYPE>(wd, sc, sc1, mn, x0, x1, (int)(int16_t)(bp & 0xFFFF), bp >> 16, bi.iv, bi.mv);
           if constexpr (DUMP) {
-            const int n = g0 + G * i;
+            const int n = row_of(i);
             if (n < rows && t < T) {
               const size_t o = ((size_t)t * rows + n) * nb + b;
               a.dbg_isum[o] = bi.iv;
@@ -272,7 +284,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
       if (slot == RC - 1 || i == steps - 1) {
         __syncthreads();
         const int nj = slot + 1, j = gl;
-        const int nr = g0 + G * (i - slot + j);
+        const int nr = row_of(i - slot + j);
         if (!DUMP && j < nj && nr < rows) {
 #pragma unroll
           for (int t = 0; t < TB; ++t) {
@@ -288,7 +300,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
       }
       return;
     }
-    const int n = g0 + G * i;
+    const int n = row_of(i);
     float v[TB];
 #pragma unroll
     for (int t = 0; t < TB; ++t) v[t] = wave_sum_width(acc[t], LPR);
@@ -332,8 +344,9 @@ static size_t gemvs_lds(int type, int K, int TB) {
   return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
 }
 
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = false, int PC = (LPR == 256 ? 3 : 2)>
-static hipError_t gos(const GemvArgs& a, hipStream_t s) {
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = false, int PC = (LPR == 256 ? 3 : 2),
+          bool SPLIT = false>
+static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
   constexpr int PF = TB == 1 ? 2 : 1;  // batch 1: two rows in flight per lane group; more tokens: registers to tokens
   // Persistent grid: PC work-groups per CU (two; three with four waves per row or where measured faster), or as many
@@ -355,7 +368,9 @@ static hipError_t gos(const GemvArgs& a, hipStream_t s) {
       n = 256;
     return n;
   }();
-  const int wgs = min(per_cu * cus, (a.w.rows + GPW - 1) / GPW);
+  const int wgs = min(per_cu * cus, (a0.w.rows + GPW - 1) / GPW);
+  GemvArgs a = a0;
+  a.split = SPLIT && wgs > cus && a.w.rows > 2 * wgs * GPW ? cus : 0;
   gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG><<<wgs, 256, AREG ? 0 : gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
@@ -416,7 +431,8 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
       } else if (a.T == 1 && nb > 512 && nb <= 768) {
         // batch 1, long rows: 128 lanes (two waves) per row, token blocks in registers: the 17408-wide down projection
         // (544 blocks) at 11.9 us against 12.3 us with four waves per row and the token row in LDS
-        e = nb <= 640 ? gos<TYPE, 128, 5, false, 1, DUMP, true>(c, s) : gos<TYPE, 128, 6, false, 1, DUMP, true>(c, s);
+        e = nb <= 640 ? gos<TYPE, 128, 5, false, 1, DUMP, true, 2, true>(c, s)
+                      : gos<TYPE, 128, 6, false, 1, DUMP, true, 2, true>(c, s);
       } else if (nb <= 256) {  // 32 lanes per row, up to 8 blocks per lane
         switch ((nb + 31) / 32) {
           case 1: e = nb == 32 ? gos_tb<TYPE, 32, 1, true, DUMP>(c, s) : gos_tb<TYPE, 32, 1, false, DUMP>(c, s); break;

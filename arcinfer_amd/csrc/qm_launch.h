@@ -27,6 +27,7 @@ struct GemvArgs {
   int ldc, c_off, accumulate;
   int32_t* dbg_isum;  // non-null: write the block sums instead of C
   int32_t* dbg_msum;
+  int split = 0;      // batch-1 sweep: work-groups of the first dispatch round (0: every group takes the same rows)
 };
 hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s);
 
