@@ -151,8 +151,8 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s03, uint32_t s47, uint32
 // The prepared header stores scales_h with bit 1 of every 2-bit field flipped, so each field read as a signed 2-bit
 // number is (high bits of ls) - 2, and (field << 4) | (low 4 bits) is ls - 32 in one sign-extending extract.
 __device__ __forceinline__ int iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
-  const int hi = (int)(h0 << (14 - 2 * ib)) >> 30;
-  return (int)((uint32_t)hi << 4 | ((h1 >> (4 * ib)) & 0xFu));
+  const int hi = __builtin_amdgcn_sbfe((int)h0, 16 + 2 * ib, 2);  // (one signed bit-field extract)
+  return (int)((uint32_t)hi << 4 | __builtin_amdgcn_ubfe(h1, 4 * ib, 4));
 }
 
 // IQ3_S sign masks: for a sign byte s, m[0]/m[1] = 0xFF in each byte whose sign bit (bits 0..3 / 4..7) is set, and

@@ -426,8 +426,12 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
         // batch 1, a small matrix (the grid has about one row per 32-lane group) with rows of more than 64 blocks (so
         // at least half of the 128 lanes have a block): 128 lanes per row, token blocks in registers, three
         // work-groups per CU. Measured against 32 lanes per row: Q8_0 4096 x 4096 6.8 -> 6.4 us,
-        // IQ3_S 5120 x 5120 7.7 -> 6.8 us, IQ4_XS 5120 x 5120 6.7 -> 6.2 us
-        e = nb <= 128 ? gos<TYPE, 128, 1, false, 1, DUMP, true, 3>(c, s) : gos<TYPE, 128, 2, false, 1, DUMP, true, 3>(c, s);
+        // IQ3_S 5120 x 5120 7.7 -> 6.8 us, IQ4_XS 5120 x 5120 6.7 -> 6.2 us. Q8_0 (32 payload bytes per block, twice the
+        // 4-bit types') with two work-groups per CU instead: 4096 x 4096 6.2 -> 5.8 us, 5120 x 5120 8.6 -> 7.9 us (A/B
+        // in one process; every 4-bit and grid type measured faster with three)
+        constexpr int PCS = TYPE == T_Q8_0 ? 2 : 3;
+        e = nb <= 128 ? gos<TYPE, 128, 1, false, 1, DUMP, true, PCS>(c, s)
+                      : gos<TYPE, 128, 2, false, 1, DUMP, true, PCS>(c, s);
       } else if (a.T == 1 && nb > 512 && nb <= 768) {
         // batch 1, long rows: 128 lanes (two waves) per row, token blocks in registers: the 17408-wide down projection
         // (544 blocks) at 11.9 us against 12.3 us with four waves per row and the token row in LDS

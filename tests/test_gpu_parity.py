@@ -170,6 +170,31 @@ def test_gemv_baseline_iq4_xs(qm, dev, N, K):
     assert_elementwise(C.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("qtype", [F.IQ4_XS, F.Q4_K, F.Q8_0, F.IQ3_S])
+@pytest.mark.parametrize("N", [2049, 3000, 5136])
+def test_gemv_long_rows_first_round_split(qm, dev, qtype, N):
+    """Batch-1 rows of 544 blocks (K = 17408) take the route whose first-dispatch-round work-groups also take the rows
+    past the lockstep sweep; row counts that leave a ragged remainder (and 2049: the split just engaged) against the
+    oracle, block sums bit-exact."""
+    import torch
+    K = 17408
+    W = F.synth_weight(qtype, N, K, seed=N + qtype)
+    x = F.synth_activations(1, K, seed=N)
+    aq, asc, absum = acts(qm, x, dev, M_stride=16)
+    w = qm.QWeight(qtype, to_dev(W, dev), N, K)
+    C = qm.gemv(w, aq, asc, absum)
+    isum, msum = qm.gemv_blocksums(w, aq, absum, T=1)
+    torch.cuda.synchronize()
+    ref, risum, rmsum = oracle.blockdot(qtype, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=1,
+                                        blocksums=True)
+    assert rel_err(C.cpu().numpy(), ref) < TOL_INT8_PATH
+    assert_elementwise(C.cpu().numpy(), ref)
+    assert np.array_equal(isum.cpu().numpy(), risum)
+    if msum is not None:
+        assert np.array_equal(msum.cpu().numpy(), rmsum)
+    w.release()
+
+
 @pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
 def test_gemv_baseline_iq4_xs_blocksums(qm, dev, N, K):
     """North-star shapes at full size: the int32 block sums of the shipped batch-1 GEMV, bit-exact."""
