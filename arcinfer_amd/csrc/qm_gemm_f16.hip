@@ -258,10 +258,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
           tq[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, tq[t], 0, 0, 0);
         }
       } else {
-        // items k = (token tile t, block bb), t = k / 2, bb = k % 2: stage k issues item k's two MFMAs, reads item
-        // k + 1's operands from LDS between them, and scales item k - 1's block sums, so one MFMA result is in flight
-        // while the previous one is consumed and the LDS round trip of the next item runs under both (579 vs 605 us on
-        // the 2048 x 5120 x 17408 shape, A/B in one process)
+        // items k = (token tile t, block bb), t = k / 2, bb = k % 2. Stage k: item k's first MFMA, item k + 1's
+        // operands read from LDS, half of item k - 1's scaling fmas, item k's second MFMA (it accumulates onto the
+        // first, so it waits for it: the eight fmas fill that wait), the other half of the fmas. One MFMA result is in
+        // flight while the previous one is consumed, and the next item's LDS round trip runs under both (605 -> 579 ->
+        // 561 us on the 2048 x 5120 x 17408 shape for the operand prefetch and then the split fmas, A/B in one process).
         f32x16 Iprev;
         f16x8 nb0 = *(const f16x8*)(L), nb1 = *(const f16x8*)(L + kF16Piece);  // (item 0)
         float nsv = DUMP ? 0.0f : sasc[cur][0][lc], svprev = 0.0f;
@@ -269,9 +270,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         for (int k = 0; k <= 8; ++k) {
           f32x16 Icur;
           float svcur = 0.0f;
+          const int bb = k & 1;
+          const f16x8 b1 = nb1;
           if (k < 8) {
-            const int bb = k & 1;
-            const f16x8 b0 = nb0, b1 = nb1;
+            const f16x8 b0 = nb0;
             svcur = nsv;
             Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][0], b0, zero16, 0, 0, 0);
             if (k + 1 < 8) {
@@ -281,12 +283,22 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
               nb1 = *(const f16x8*)(Lt + (2 * bb1 + 1) * kF16Piece);
               if constexpr (!DUMP) nsv = sasc[cur][bb1][32 * t1 + lc];
             }
-            Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, Icur, 0, 0, 0);
           }
+          __builtin_amdgcn_sched_barrier(0);
+          const int tp = (k - 1) >> 1, bbp = (k - 1) & 1;
+          if constexpr (!DUMP) {
+            if (k > 0) {
+#pragma unroll
+              for (int r = 0; r < 8; ++r)
+                tq[tp][r] = (p == 0 && bbp == 0) ? svprev * Iprev[r] : fmaf(svprev, Iprev[r], tq[tp][r]);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (k < 8) Icur = __builtin_amdgcn_mfma_f32_32x32x16_f16(aw[bb][1], b1, Icur, 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
           if (k > 0) {
-            const int t = (k - 1) >> 1, bb = (k - 1) & 1;
             if constexpr (DUMP) {
-              const int m = m0 + 32 * t + lc, blk = 8 * s + 2 * p + bb;
+              const int m = m0 + 32 * tp + lc, blk = 8 * s + 2 * p + bbp;
 #pragma unroll
               for (int r = 0; r < 16; ++r) {
                 const int n = nbase + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -294,12 +306,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
               }
             } else {
 #pragma unroll
-              for (int r = 0; r < 16; ++r)
-                tq[t][r] = (p == 0 && bb == 0) ? svprev * Iprev[r] : fmaf(svprev, Iprev[r], tq[t][r]);
+              for (int r = 8; r < 16; ++r)
+                tq[tp][r] = (p == 0 && bbp == 0) ? svprev * Iprev[r] : fmaf(svprev, Iprev[r], tq[tp][r]);
               // (pins the scaled sums here: otherwise the compiler defers every fma to the superblock end and keeps
               // each block's MFMA result alive meanwhile, in scratch memory)
 #pragma unroll
-              for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(tq[t][r]));
+              for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(tq[tp][r]));
             }
           }
           if (k < 8) {
