@@ -117,7 +117,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 //
 // AREG (batch 1 only): lane j reads the same blocks of the token row for every weight row, so it loads them once into
 // registers (two 16-byte words, the scale and the Q4_K / Q5_K / Q6_K sums per block) and nothing is staged in LDS.
-template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP, bool AREG = false, int NT = 256>
+template <int TYPE, int LPR, int CH, bool EXACT, int TB, int PF, bool DUMP, bool AREG = false, int NT = 256,
+          bool SPLIT = false>
 __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   static_assert(!AREG || TB == 1, "token blocks in registers: batch 1 only");
   extern __shared__ uint4 smem[];
@@ -140,7 +141,8 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   // remaining rows: the second work-group on a CU issues its loads behind the first one's, so its rows arrive about
   // two row steps later; on the 17408-wide down projection the two rounds then end together (12.4 vs 13.0 us in a
   // launch loop on one box).
-  const int split = a.split, G1 = split * GPW;
+  // (a compile-time switch: the split's row mapping costs registers that the multi-token instantiations need)
+  const int split = SPLIT ? a.split : 0, G1 = split * GPW;
   const int s2 = split > 0 ? max(1, (rows + G - 1) / G - 2) : (rows + G - 1) / G;
   auto row_of = [&](int i) { return i < s2 ? g0 + G * i : G * s2 + g0 + G1 * (i - s2); };
   auto steps_of = [&](int g) {
@@ -356,7 +358,7 @@ static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   static const int per_cu = [] {
     int n = 0;
     const size_t lds_max = AREG ? 0 : gemvs_lds(TYPE, 32 * LPR * CH, TB);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false, AREG>, 256, lds_max) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false, AREG, 256, SPLIT>, 256, lds_max) !=
             hipSuccess || n < 1)
       n = 1;
     return min(PC, n);
@@ -371,7 +373,7 @@ static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   const int wgs = min(per_cu * cus, (a0.w.rows + GPW - 1) / GPW);
   GemvArgs a = a0;
   a.split = SPLIT && wgs > cus && a.w.rows > 2 * wgs * GPW ? cus : 0;
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG><<<wgs, 256, AREG ? 0 : gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG, 256, SPLIT><<<wgs, 256, AREG ? 0 : gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
 
