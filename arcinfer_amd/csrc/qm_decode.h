@@ -94,6 +94,13 @@ __device__ __forceinline__ RawBlk load_block(const WView& w, int n, int b) {
   return load_block_at<TYPE>(w.qs + (size_t)n * (w.K / 32) * Tr::QB, w.hdr + (size_t)n * (w.K / 256) * Tr::HB, b);
 }
 
+// x >> 4 as one 64-bit shift (the compiler would split it into two 32-bit shifts where only masked bits differ)
+__device__ __forceinline__ uint64_t shr64_4(uint64_t x) {
+  uint64_t r;
+  asm("v_lshrrev_b64 %0, 4, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // Decodes a loaded 32-block (index ib = b % 8 in its superblock): w[k] = elements 4k..4k+3 (int8x4), the integer
 // scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K, IQ2_XS and IQ2_S), the min mn, the float scales d (and dmin). Q6_K's
 // values come out as the stored 6-bit numbers 0..63 (the offset of 32 is removed by block_product).
@@ -166,10 +173,14 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     q4k_scale_min(r.h.y, r.h.z, r.h.w, ib, sc, mn);
   } else if constexpr (TYPE == T_IQ4_XS) {
     const uint32_t qq[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
+    // high nibbles: one 64-bit shift serves two words (the bits shifted in from the upper word land in the masked-out
+    // top nibble)
+    const uint64_t s01 = shr64_4((uint64_t)r.q0.y << 32 | r.q0.x), s23 = shr64_4((uint64_t)r.q0.w << 32 | r.q0.z);
+    const uint32_t qh[4] = {(uint32_t)s01, (uint32_t)(s01 >> 32), (uint32_t)s23, (uint32_t)(s23 >> 32)};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       wd[k] = kv_lookup4(kv, qq[k] & 0x0F0F0F0Fu);
-      wd[4 + k] = kv_lookup4(kv, (qq[k] >> 4) & 0x0F0F0F0Fu);
+      wd[4 + k] = kv_lookup4(kv, qh[k] & 0x0F0F0F0Fu);
     }
     d = h2f(r.h.x);
     sc = iq4xs_scale(r.h.x, r.h.y, ib);

@@ -152,7 +152,7 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s03, uint32_t s47, uint32
 // number is (high bits of ls) - 2, and (field << 4) | (low 4 bits) is ls - 32 in one sign-extending extract.
 __device__ __forceinline__ int iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
   const int hi = __builtin_amdgcn_sbfe((int)h0, 16 + 2 * ib, 2);  // (one signed bit-field extract)
-  return (int)((uint32_t)hi << 4 | __builtin_amdgcn_ubfe(h1, 4 * ib, 4));
+  return hi * 16 + (int)__builtin_amdgcn_ubfe(h1, 4 * ib, 4);
 }
 
 // IQ3_S sign masks: for a sign byte s, m[0]/m[1] = 0xFF in each byte whose sign bit (bits 0..3 / 4..7) is set, and

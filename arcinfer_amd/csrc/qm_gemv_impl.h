@@ -350,7 +350,9 @@ template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = 
           bool SPLIT = false>
 static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
-  constexpr int PF = TB == 1 ? 2 : 1;  // batch 1: two rows in flight per lane group; more tokens: registers to tokens
+  // batch 1: two rows in flight per lane group (three measured slower: 11.7 -> 13.0 us on the down projection,
+  // 10.7 -> 12.3 on gate/up); more tokens: registers to tokens
+  constexpr int PF = TB == 1 ? 2 : 1;
   // Persistent grid: PC work-groups per CU (two; three with four waves per row or where measured faster), or as many
   // as the kernel's registers and LDS let reside (the 8-token instantiation needs more than 256 registers: one wave per
   // SIMD), so the whole grid is resident at once; fewer when the matrix has fewer rows than lane groups. Occupancy is

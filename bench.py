@@ -35,6 +35,9 @@ def parse():
     # (2000 warm-up steps, ~50 ms of GEMV work: the GPU's clocks settle under load within tens of milliseconds; with 20
     #  the timed steps ran ~15 % slower while the clocks were still rising)
     p.add_argument("--warmup", type=int, default=2000)
+    # (the GPU's clocks rise over tens of milliseconds of load: each leg first replays its warm-up untimed for at
+    #  least this long, whatever --warmup says, so short warm-ups do not time a GPU that is still clocking up)
+    p.add_argument("--settle-ms", type=float, default=300.0)
     p.add_argument("--only", choices=["all", "gemv", "gemm", "moe", "report"], default="all")
     p.add_argument("--copies", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -44,8 +47,24 @@ def parse():
     return p.parse_args()
 
 
+SETTLE_S = 0.3
+
+
+def settle(fn):
+    """Run fn untimed until SETTLE_S seconds of wall time have passed (at least once)."""
+    import torch
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= SETTLE_S:
+            return
+
+
 def timed(fn, steps, warmup, stream, pre=None):
     import torch
+    if SETTLE_S > 0:
+        settle(lambda: [fn(i) for i in range(max(1, warmup))])
     for i in range(warmup):
         fn(i)
     if pre is not None:
@@ -80,6 +99,8 @@ def timed_graph(fn, args, stream):
         fn(i)  # (first-launch work stays out of the captures)
     torch.cuda.synchronize()
     gw, gt = graphed(fn, max(1, args.warmup)), graphed(fn, args.steps)
+    if SETTLE_S > 0:
+        settle(gw.replay)
     ms, _ = timed(lambda i: gt.replay(), 1, 0, stream, pre=gw.replay)
     return ms / args.steps
 
@@ -99,6 +120,8 @@ def profile_traffic(kernel_key):
 
 def main():
     args = parse()
+    global SETTLE_S
+    SETTLE_S = 0.0 if args.profile else args.settle_ms / 1e3
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the multi-GPU design is "
               "described in DESIGN.md, not built)", file=sys.stderr)
@@ -113,7 +136,7 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     out = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+           "ms_per_step": None, "settle_ms": args.settle_ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
            "data": "synthetic (seeded GGUF-format weights, N(0,1) activations; BASELINE.json configs)",
            "config": {"workload": "IQ4_XS decode GEMV, batch 1: K=5120->N=17408 and K=17408->N=5120 per step, "
                                   f"{args.copies} rotating weight copies each", "parallelism": "none (1 GPU)"}}
