@@ -36,7 +36,8 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool known_type(int t) {
   return t == QM_Q4_0 || t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q5_K || t == QM_Q6_K || t == QM_IQ4_NL || t == QM_IQ3_S ||
-         t == QM_IQ4_XS || t == QM_IQ2_XXS || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_IQ3_XXS;
+         t == QM_IQ4_XS || t == QM_IQ2_XXS || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_IQ3_XXS || t == QM_Q3_K ||
+         t == QM_Q2_0;
 }
 
 int payload_bytes(int t) {
@@ -44,15 +45,15 @@ int payload_bytes(int t) {
     case QM_Q8_0: return 32;
     case QM_Q6_K: return 24;
     case QM_Q5_K: return 20;
-    case QM_IQ3_S: case QM_IQ3_XXS: return 12;
-    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: return 8;
+    case QM_IQ3_S: case QM_IQ3_XXS: case QM_Q3_K: return 12;
+    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: case QM_Q2_0: return 8;
     default: return 16;
   }
 }
 int header_bytes(int t) {
   switch (t) {
-    case QM_IQ4_XS: return 8;
-    case QM_Q6_K: case QM_IQ2_S: return 20;
+    case QM_IQ4_XS: case QM_Q2_0: return 8;
+    case QM_Q6_K: case QM_IQ2_S: case QM_Q3_K: return 20;
     case QM_IQ2_XS: return 12;
     case QM_IQ2_XXS: case QM_IQ3_XXS: return 4;
     default: return 16;
@@ -61,9 +62,12 @@ int header_bytes(int t) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// the types of 32-element blocks, whose rows may end inside a superblock (padded with zero blocks when prepared)
-bool small_block_type(int t) { return t == QM_Q8_0 || t == QM_Q4_0 || t == QM_IQ4_NL; }
-bool row_length_ok(int t, int K) { return K > 0 && (K % 256 == 0 || (small_block_type(t) && K % 32 == 0)); }
+// the types of 32- (Q2_0: 64-) element blocks, whose rows may end inside a superblock (padded with zero blocks when
+// prepared)
+bool small_block_type(int t) { return t == QM_Q8_0 || t == QM_Q4_0 || t == QM_IQ4_NL || t == QM_Q2_0; }
+bool row_length_ok(int t, int K) {
+  return K > 0 && (K % 256 == 0 || (small_block_type(t) && K % (t == QM_Q2_0 ? 64 : 32) == 0));
+}
 int padded_k(int K) { return (K + 255) / 256 * 256; }
 
 
@@ -163,6 +167,8 @@ size_t qmatmul_sb_bytes(int type) {
     case QM_IQ2_XS: return 74;
     case QM_IQ2_S: return 82;
     case QM_IQ3_XXS: return 98;
+    case QM_Q3_K: return 110;
+    case QM_Q2_0: return 72;
     default: return 0;
   }
 }
@@ -181,7 +187,7 @@ int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int row
   if (rows <= 0 || !row_length_ok(type, K))
     return fail(QM_ERR_SHAPE,
                 "qmatmul_prepare_weight: rows %d, K %d (K must be a positive multiple of 256, or of 32 for Q8_0, "
-                "Q4_0 and IQ4_NL)", rows, K);
+                "Q4_0 and IQ4_NL, of 64 for Q2_0)", rows, K);
   QM_CHECK_INIT();
   hipStream_t s = (hipStream_t)stream;
   const int kraw = K / 32;  // 32-blocks per raw row
@@ -596,7 +602,7 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
     e = qm::launch_moe_scatter(ids, wts, T, NU, NE, part, counts, cursor, tstart, tiles, L.tile_rows, stok, swt, inv, s);
   // gate and up: one launch when they share a type the int8 kernel takes in one pass; otherwise the gate projection
   // into hf, then the up projection forming h from it
-  const bool s16 = [](int t) { return t == QM_Q6_K || t == QM_IQ2_XS || t == QM_IQ2_S; }(gate->type);
+  const bool s16 = [](int t) { return t == QM_Q6_K || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_Q3_K; }(gate->type);
   const bool fused = gate->type == up->type && !s16;
   if (e == hipSuccess) {
     qm::GemmArgs a{};

@@ -42,6 +42,16 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
   } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
     r.q0 = ld_stream16(qp);
     r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (TYPE == T_Q2_0) {
+    const uint32_t* q = (const uint32_t*)qp;
+    r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), 0u, 0u};
+    r.h.x = ((const uint16_t*)hp)[block_scale_slot<TYPE>(b & 7)];
+  } else if constexpr (TYPE == T_Q3_K) {
+    const uint32_t* q = (const uint32_t*)qp;
+    r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2),
+                   0u};
+    r.h.x = ((const uint16_t*)hp)[b & 7];  // the block's two int8 scales
+    r.h.y = ((const uint16_t*)hp)[8];      // f16 d
   } else if constexpr (TYPE == T_Q5_K) {
     r.q0 = ld_stream16(qp);
     r.q1.x = __builtin_nontemporal_load((const uint32_t*)(qp + 16));
@@ -125,7 +135,20 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     d = h2f(r.h.y);
     return;
   }
-  if constexpr (TYPE == T_Q8_0) {
+  if constexpr (TYPE == T_Q3_K) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wd[k] = q3_word(r.q0.x, r.q0.y, r.q0.z, k);
+    sc = (int)(int8_t)(r.h.x & 0xFFu);
+    sc1 = (int)(int8_t)((r.h.x >> 8) & 0xFFu);
+    d = h2f(r.h.y);
+    return;
+  }
+  if constexpr (TYPE == T_Q2_0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wd[k] = q2_word(r.q0.x, r.q0.y, k);
+    d = h2f(r.h.x);
+    sc = 1;
+  } else if constexpr (TYPE == T_Q8_0) {
     wd[0] = r.q0.x; wd[1] = r.q0.y; wd[2] = r.q0.z; wd[3] = r.q0.w;
     wd[4] = r.q1.x; wd[5] = r.q1.y; wd[6] = r.q1.z; wd[7] = r.q1.w;
     d = h2f(r.h.x);

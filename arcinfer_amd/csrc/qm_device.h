@@ -19,6 +19,11 @@
 //   IQ2_XS  QB 8: GGUF qs[4] (u16: 9-bit grid index | 7-bit sign index << 9)  HB 12: scales[8], f16 d, 2 zero
 //   IQ2_S   QB 8: 4 grid index low bytes, 4 sign bytes          HB 20: qh[8], scales[8], f16 d, 2 zero
 //   IQ3_XXS QB 12: 8 grid index bytes, GGUF sign/scale word (4 x 7-bit sign indices, 4-bit scale)  HB 4: f16 d, 2 zero
+//   Q3_K   QB 12: two words of 2-bit fields, then a word of high bits: word h (h = 0, 1), byte i, bits 2j..2j+1 = the
+//                 low 2 bits of element 4 (4h + j) + i; word 2, byte i, bit k = the high bit (GGUF hmask) of element
+//                 4k + i. Value = (low | high << 2) - 4            HB 20: int8 scales[16] (6-bit - 32), f16 d, 2 zero
+//   Q2_0   QB 8: two words of 2-bit codes laid out as Q3_K's first two; value = code - 1
+//                 HB 8: the four 64-blocks' f16 d (a 32-block uses its 64-block's: half-block b -> scale b / 2)
 // (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
 // (Q4_K's GGUF nibble order -- 64-element chunks, low nibbles first -- is regrouped to IQ4_XS's per-32 order, so
 // the 4-bit types share one unpacking path.)
@@ -33,7 +38,7 @@ namespace qm {
 
 enum : int {
   T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17, T_IQ3_XXS = 18,
-  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23
+  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_Q3_K = 11, T_Q2_0 = 42
 };
 
 template <int TYPE> struct Traits;
@@ -52,8 +57,12 @@ template <> struct Traits<T_IQ2_XXS> { static constexpr int QB = 8, HB = 4, GGUF
 template <> struct Traits<T_IQ2_XS> { static constexpr int QB = 8, HB = 12, GGUF_SB = 74; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_IQ2_S> { static constexpr int QB = 8, HB = 20, GGUF_SB = 82; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_IQ3_XXS> { static constexpr int QB = 12, HB = 4, GGUF_SB = 98; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
-// per-32 f16 scales in the header (Q8_0's layout), no integer sub-scales
-template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL;
+template <> struct Traits<T_Q3_K> { static constexpr int QB = 12, HB = 20, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
+template <> struct Traits<T_Q2_0> { static constexpr int QB = 8, HB = 8, GGUF_SB = 72; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+// f16 scales per 32-block in the header (Q8_0's layout; Q2_0: one per 64-block), no integer sub-scales
+template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL || TYPE == T_Q2_0;
+// the header's f16 scale of 32-block b (0..7) for kBlockScales types: its index among the header's halfwords
+template <int TYPE> __host__ __device__ constexpr int block_scale_slot(int b) { return TYPE == T_Q2_0 ? b >> 1 : b; }
 // whether the kernels need the per-16 activation sums (absum)
 template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
 // the codebook types whose tables live in LDS
@@ -339,4 +348,16 @@ __device__ __forceinline__ float wave_max(float v) {
 namespace qm {
 // n - 8 for four nibble values 0..15 held one per byte: a byte-wise subtract without borrows
 __device__ __forceinline__ uint32_t sub8_bytes(uint32_t n) { return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
+// Q2_0 / Q3_K (prepared layout above): word k (elements 4k..4k+3) of a 32-block as four signed bytes.
+//   Q2_0: code - 1 by a byte permute of the table {-1, 0, 1, 2}; Q3_K: (low | high << 2) - 4 by a permute of
+//   {-4, ..., 3}. d01: the payload's two words of 2-bit fields, hw: Q3_K's word of high bits.
+__device__ __forceinline__ uint32_t q2_word(uint32_t d0, uint32_t d1, int k) {
+  const uint32_t c = ((k < 4 ? d0 : d1) >> (2 * (k & 3))) & 0x03030303u;
+  return __builtin_amdgcn_perm(0u, 0x020100FFu, c);
+}
+__device__ __forceinline__ uint32_t q3_word(uint32_t d0, uint32_t d1, uint32_t hw, int k) {
+  const uint32_t c = (((k < 4 ? d0 : d1) >> (2 * (k & 3))) & 0x03030303u) | (((hw >> k) & 0x01010101u) << 2);
+  return __builtin_amdgcn_perm(0x03020100u, 0xFFFEFDFCu, c);
+}
 }  // namespace qm

@@ -73,7 +73,7 @@ __device__ __forceinline__ uint4 load_payload(const WView& w, int n, int blk, in
 template <int TYPE>
 __device__ __forceinline__ uint4 load_header(const WView& w, int n, int s) {
   const uint8_t* hp = w.hdr + ((size_t)n * (w.K / 256) + s) * Traits<TYPE>::HB;
-  if constexpr (TYPE == T_IQ4_XS) {
+  if constexpr (Traits<TYPE>::HB == 8) {
     const uint2 h = *(const uint2*)hp;
     return make_uint4(h.x, h.y, 0u, 0u);
   } else if constexpr (Traits<TYPE>::HB == 4) {
@@ -90,6 +90,10 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
   v4i r;
   if constexpr (TYPE == T_Q8_0) {
     r[0] = (int)q.x; r[1] = (int)q.y; r[2] = (int)q.z; r[3] = (int)q.w;
+  } else if constexpr (TYPE == T_Q2_0) {
+    // (k-half hf: words 4 hf .. 4 hf + 3, all four from payload word hf)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = (int)q2_word(q.x, q.y, 4 * hf + k);
   } else if constexpr (TYPE == T_Q5_K) {
     // (fifth bits: byte i, bit k = element 4k+i of the first half, bit 4+k = of the second)
     r[0] = (int)(q.x & 0x0F0F0F0Fu); r[1] = (int)(q.y & 0x0F0F0F0Fu);
@@ -142,7 +146,8 @@ __device__ __forceinline__ void sb_scales(uint4 h, const uint4* pay, float dsc[8
     const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      dsc[b] = h2f(hh[b >> 1] >> (16 * (b & 1)));
+      const int j = block_scale_slot<TYPE>(b);
+      dsc[b] = h2f(hh[j >> 1] >> (16 * (j & 1)));
       dmn[b] = 0.0f;
       isc[b] = 1;
     }
@@ -642,7 +647,8 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     }
   };
   // this lane's share of a block: Q6_K nibble bytes 8h..8h+7 and both 2-bit words (record: 16 nibble bytes, 2
-  // words); IQ2_XS / IQ2_S the block's whole 8-byte record (nib)
+  // words); Q3_K its whole record (nib: the 2-bit words, hw.x: the high bits); IQ2_XS / IQ2_S the block's whole
+  // 8-byte record (nib)
   const uint8_t* qrow = a.w.qs + (size_t)n * nb * Tr::QB;
   const uint8_t* hrow = a.w.hdr + (size_t)n * nsb * Tr::HB;
   auto load_blk = [&](int blk, uint2& nib, uint2& hw) {
@@ -650,6 +656,9 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     if constexpr (TYPE == T_Q6_K) {
       nib = *(const uint2*)(r + 8 * hf);
       hw = *(const uint2*)(r + 16);
+    } else if constexpr (TYPE == T_Q3_K) {  // (the block's two words of 2-bit fields and its word of high bits)
+      nib = *(const uint2*)r;
+      hw = make_uint2(*(const uint32_t*)(r + 8), 0u);
     } else {
       nib = *(const uint2*)r;
       hw = make_uint2(0u, 0u);
@@ -658,7 +667,7 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
   uint2 nib[8], hw[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) load_blk(b, nib[b], hw[b]);
-  // (header records are 20 or 12 bytes: 4-byte aligned, so read as dwords) sc: Q6_K int8 scales[16], IQ2_XS
+  // (header records are 20 or 12 bytes: 4-byte aligned, so read as dwords) sc: Q6_K / Q3_K int8 scales[16], IQ2_XS
   // scales[8] (.x .y), IQ2_S qh[8] (.x .y) and scales[8] (.z .w); dd: f16 d
   auto load_hdr = [&](int sb, uint4& sc, uint32_t& dd) {
     const uint32_t* h = (const uint32_t*)(hrow + (size_t)sb * Tr::HB);
@@ -691,7 +700,7 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     const int sn = s + 1 < nsb ? s + 1 : s;
     fetch(sn);
     const uint32_t scw[4] = {hsc.x, hsc.y, hsc.z, hsc.w};
-    const float d = TYPE == T_Q6_K ? h2f(hd) : h2f(hd) * kIqDScale<TYPE>;
+    const float d = (TYPE == T_Q6_K || TYPE == T_Q3_K) ? h2f(hd) : h2f(hd) * kIqDScale<TYPE>;
     load_hdr(sn, hsc, hd);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -707,6 +716,13 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
         w[3] = ((nib[b].y >> 4) & 0x0F0F0F0Fu) | ((B2 >> 2) & 0x30303030u);
 #pragma unroll
         for (int k = 0; k < 4; ++k) w[k] = ((w[k] | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
+        sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
+      } else if constexpr (TYPE == T_Q3_K) {
+        w[0] = q3_word(nib[b].x, nib[b].y, hw[b].x, 2 * hf);
+        w[1] = q3_word(nib[b].x, nib[b].y, hw[b].x, 2 * hf + 1);
+        w[2] = q3_word(nib[b].x, nib[b].y, hw[b].x, 4 + 2 * hf);
+        w[3] = q3_word(nib[b].x, nib[b].y, hw[b].x, 5 + 2 * hf);
         sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
         sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
       } else {
@@ -997,6 +1013,7 @@ static hipError_t dispatch_s16(int mode, const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
   switch (type) {
     case T_Q6_K: return dispatch_s16<T_Q6_K>(mode, a, s);
+    case T_Q3_K: return dispatch_s16<T_Q3_K>(mode, a, s);
     case T_IQ2_XS: return dispatch_s16<T_IQ2_XS>(mode, a, s);
     case T_IQ2_S: return dispatch_s16<T_IQ2_S>(mode, a, s);
     default: break;
@@ -1007,6 +1024,7 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
     case T_IQ4_XS: return dispatch<T_IQ4_XS>(mode, a, s);
     case T_IQ3_S: return dispatch<T_IQ3_S>(mode, a, s);
     case T_Q4_0: return dispatch<T_Q4_0>(mode, a, s);
+    case T_Q2_0: return dispatch<T_Q2_0>(mode, a, s);
     case T_IQ4_NL: return dispatch<T_IQ4_NL>(mode, a, s);
     case T_Q5_K: return mode == GEMM_DENSE ? dispatch<T_Q5_K>(mode, a, s) : hipErrorInvalidValue;
     case T_IQ2_XXS: return dispatch<T_IQ2_XXS>(mode, a, s);

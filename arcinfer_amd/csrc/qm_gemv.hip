@@ -19,6 +19,8 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_IQ2_XS: return gemv_dispatch<T_IQ2_XS>(a, s);
     case T_IQ2_S: return gemv_dispatch<T_IQ2_S>(a, s);
     case T_IQ3_XXS: return gemv_dispatch<T_IQ3_XXS>(a, s);
+    case T_Q3_K: return gemv_dispatch<T_Q3_K>(a, s);
+    case T_Q2_0: return gemv_dispatch<T_Q2_0>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

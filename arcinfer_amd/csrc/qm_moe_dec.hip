@@ -268,6 +268,7 @@ static hipError_t down_typed(int T, int NU, int E, int F, const WView& down, con
 // the expert types of the MoE paths: one integer (or f16) scale per 16 or 32 and no per-block mins, as the
 // reference's moe_rg (zero/engine_moe.h:297-301)
 #define QM_MOE_TYPES(X) X(T_Q8_0) X(T_Q4_0) X(T_IQ4_NL) X(T_IQ4_XS) X(T_IQ3_S) X(T_IQ2_XXS) X(T_IQ2_XS) X(T_IQ2_S) \
+  X(T_Q3_K) X(T_Q2_0) \
   X(T_IQ3_XXS) X(T_Q6_K)
 
 template <int MODE>

@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
   const long n = i / nsb;
   const int s = (int)(i % nsb);
   // (the small-block types: raw rows of kraw blocks of Tr::GGUF_SB / 8 bytes; the others: rows of nsb superblocks)
-  constexpr bool small = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL;
+  constexpr bool small = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL || TYPE == T_Q2_0;
   const size_t row_bytes = small ? (size_t)kraw * (Tr::GGUF_SB / 8) : (size_t)nsb * Tr::GGUF_SB;
   const uint8_t* p = raw + (size_t)n * row_bytes + (size_t)s * Tr::GGUF_SB;
   const int nblk = min(8, kraw - 8 * s);  // blocks of this superblock present in the raw row
@@ -84,6 +84,49 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
       h[2 * b + 1] = in ? p[18 * b + 1] : 0;
       for (int t = 0; t < 16; ++t) q[16 * b + t] = in ? p[18 * b + 2 + t] : 0;
     }
+  } else if constexpr (TYPE == T_Q2_0) {
+    // 4 GGUF blocks of (f16 d, 16 code bytes: element e of the 64 in bits 2 (e % 4) of byte e / 4), value (code - 1) d
+    // (src/quants.h:540-548; decode.cl:248-256); 32-block b is half b % 2 of block b / 2. Blocks past the raw row
+    // stay all zero (scale 0), as pad_small_block_rows writes them.
+    for (int t = 0; t < 8 * Tr::QB; ++t) q[t] = 0;
+    for (int g = 0; g < 4; ++g) {
+      const bool in = 2 * g < nblk;
+      h[2 * g] = in ? p[18 * g] : 0;
+      h[2 * g + 1] = in ? p[18 * g + 1] : 0;
+      if (!in) continue;
+      for (int hb = 0; hb < 2; ++hb) {
+        uint8_t* dst = q + Tr::QB * (2 * g + hb);
+        for (int e = 0; e < 32; ++e) {
+          const int E = 32 * hb + e, k = e >> 2, i = e & 3;
+          const int c = (p[18 * g + 2 + E / 4] >> (2 * (E % 4))) & 3;
+          dst[4 * (k >> 2) + i] |= (uint8_t)(c << (2 * (k & 3)));
+        }
+      }
+    }
+  } else if constexpr (TYPE == T_Q3_K) {
+    // hmask[32] | qs[64] | scales[12] | d (src/quants.h:465-494; decode.cl:162-176): element e of 32-block ib has the
+    // low 2 bits (qs[32 (ib / 4) + e] >> 2 (ib % 4)) & 3 and the high bit (hmask[e] >> ib) & 1, value (low | high << 2)
+    // - 4; scale i of 16 elements: low 4 bits from scales[i % 8] (nibble i / 8), top 2 bits from scales[8 + i % 4]
+    // (bits 2 (i / 4)), minus 32
+    const uint8_t *hm = p, *qs = p + 32, *sc = p + 96;
+    for (int t = 0; t < 8 * Tr::QB; ++t) q[t] = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+      uint8_t* dst = q + Tr::QB * ib;
+      for (int e = 0; e < 32; ++e) {
+        const int lo = (qs[32 * (ib >> 2) + e] >> (2 * (ib & 3))) & 3, hi = (hm[e] >> ib) & 1;
+        const int k = e >> 2, i = e & 3;
+        dst[4 * (k >> 2) + i] |= (uint8_t)(lo << (2 * (k & 3)));
+        dst[8 + i] |= (uint8_t)(hi << k);
+      }
+    }
+    for (int i = 0; i < 16; ++i) {
+      const int v = ((sc[i & 7] >> (4 * (i >> 3))) & 0xF) | (((sc[8 + (i & 3)] >> (2 * (i >> 2))) & 3) << 4);
+      h[i] = (uint8_t)(v - 32);
+    }
+    h[16] = p[108];
+    h[17] = p[109];
+    h[18] = 0;
+    h[19] = 0;
   } else if constexpr (TYPE == T_Q6_K) {
     // ql[128] | qh[64] | scales[16] | d (src/quants.h:115-135): element 128n + 32c + l has its low 4 bits in
     // ql[64n + l + 32 (c & 1)] (nibble c >> 1) and its high 2 bits in qh[32n + l] (bits 2c..2c+1); block b = 4n + c
@@ -170,6 +213,8 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, int kraw
     case T_IQ4_XS: repack_kernel<T_IQ4_XS><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q3_K: repack_kernel<T_Q3_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q2_0: repack_kernel<T_Q2_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_IQ4_NL: repack_kernel<T_IQ4_NL><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;

@@ -119,7 +119,7 @@ def _stream(stream):
 
 class QWeight:
     """A prepared weight (qm_weight*) from GGUF bytes: a uint8 tensor (device or CPU) or a numpy array. K is the raw
-    row length; Q8_0 / Q4_0 / IQ4_NL rows of K % 256 != 0 are padded with zero blocks, and self.K is then the
+    row length; Q8_0 / Q4_0 / IQ4_NL / Q2_0 rows of K % 256 != 0 are padded with zero blocks, and self.K is then the
     prepared (padded) length, self.K_raw the given one."""
 
     def __init__(self, qtype, raw, rows, K, stream=None):

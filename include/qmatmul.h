@@ -18,7 +18,8 @@
  *
  * Weights: GGUF blocks, rows of K elements, K a multiple of 256 (Q8_0: 8 blocks of 32 per 256). A weight is
  * prepared once (qmatmul_prepare_weight) into this library's own device layout and then read by every product.
- * Rows of the 32-element block types (Q8_0, Q4_0, IQ4_NL) may have any K % 32 == 0: they are padded at preparation
+ * Rows of the 32-element block types (Q8_0, Q4_0, IQ4_NL) may have any K % 32 == 0, rows of Q2_0 (the reference's
+ * own 64-element blocks, src/gguf.h:26) any K % 64 == 0: they are padded at preparation
  * with zero blocks to the next multiple of 256, which is then the weight's K (qmatmul_weight_info); the activations
  * of such a weight are K values long, the padding zeros.
  *
@@ -42,7 +43,7 @@ extern "C" {
 /* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
 typedef enum {
   QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ2_XXS = 16, QM_IQ2_XS = 17,
-  QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23
+  QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23, QM_Q3_K = 11, QM_Q2_0 = 42
 } qm_type;
 
 typedef enum {
@@ -69,14 +70,16 @@ const char* qmatmul_last_error(void);
 size_t qmatmul_sb_bytes(int type);
 
 /* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S, Q6_K,
- * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock; a padded Q8_0 / Q4_0 / IQ4_NL row counts its zero blocks). */
+ * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock and 6 per Q3_K superblock; a padded Q8_0 / Q4_0 / IQ4_NL / Q2_0
+ * row counts its zero blocks). */
 size_t qmatmul_weight_bytes(int type, int rows, int K);
 
 /* Prepares a weight from its GGUF bytes: rows x (K/256) superblocks, row-major, as stored in a GGUF tensor (a
  * stacked expert tensor [NE][N][K] is NE*N rows). raw is a device pointer if raw_on_device, else a host pointer.
  * Allocates the prepared copy and returns it in *out. Replaces Engine::make_weight / upload_padded
  * (zero/engine.h:1936-2014; src/quants.h:643-681). Q8_0, Q4_0 and IQ4_NL rows may be K % 32 == 0 long (rows of
- * K/32 GGUF blocks): they are padded with zero blocks to K rounded up to 256, as the reference's load_w_pad /
+ * K/32 GGUF blocks), Q2_0 rows K % 64 == 0 long: they are padded with zero blocks to K rounded up to 256, as the
+ * reference's load_w_pad /
  * pad_small_block_rows (zero/engine.h:2102-2116; src/quants.h:581-595); every other type needs K % 256 == 0. */
 int qmatmul_prepare_weight(int type, const void* raw, int raw_on_device, int rows, int K, void* stream,
                            qm_weight** out);
@@ -188,13 +191,13 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
  * (zero/engine_moe.h:8-282):
  *   x[t][:E] (op)= sum_k w_tk * down_e( q( silu(gate_e(a_t)) * up_e(a_t) ) ),  e = k-th expert of token t
  * gate, up: NE*Fv rows of E; down: NE*E rows of F (stacked experts), F = Fv, or F = Fv rounded up to 256 for a down
- * projection prepared from Fv-long Q8_0 / Q4_0 / IQ4_NL rows (zero-padded; the h rows then have F values, the last
+ * projection prepared from Fv-long Q8_0 / Q4_0 / IQ4_NL / Q2_0 rows (zero-padded; the h rows then have F values, the last
  * F - Fv zero: Flash Next's 640-wide experts as 768, zero/engine_moe.h:12, 318-326). a_t: token t of aq/asc (E values). q(): the h
  * rows quantized per 32 as moe_quant (moe.cl:251-282). Route, exclusive scan into tiles, device-side scatter of
  * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
  * order (moe.cl:332-340); at decode sizes (T * NU <= 64) GEMV-shaped expert kernels instead. Gate, up and down each
- * have their own type, any of Q8_0, Q4_0, IQ4_NL, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, Q6_K -- the types of
- * the reference's expert GEMM moe_rg (zero/engine_moe.h:297-306); types with per-block mins (Q4_K, Q5_K) return
+ * have their own type, any of Q8_0, Q4_0, IQ4_NL, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, Q6_K, Q3_K, Q2_0 --
+ * the types of the reference's expert GEMM moe_rg (zero/engine_moe.h:297-306); types with per-block mins (Q4_K, Q5_K) return
  * QM_ERR_TYPE, as there. accumulate 0 or 1.
  * ws: device workspace of at least qmatmul_moe_workspace_size bytes (layout: qmatmul_moe_ws_layout). */
 int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,

@@ -68,7 +68,7 @@ uint16_t qref_f32_to_fp16(float x) {
   return (uint16_t)h;
 }
 
-/* src/gguf.h:43-72 (the four types of this path) */
+/* src/gguf.h:43-72 (the block geometry of the path's types) */
 int qref_block_info(int type, int* blk, int* bytes) {
   switch (type) {
     case QREF_Q8_0: *blk = 32; *bytes = 34; return 0;
@@ -83,6 +83,8 @@ int qref_block_info(int type, int* blk, int* bytes) {
     case QREF_IQ2_XS: *blk = 256; *bytes = 74; return 0;
     case QREF_IQ2_S: *blk = 256; *bytes = 82; return 0;
     case QREF_IQ3_XXS: *blk = 256; *bytes = 98; return 0;
+    case QREF_Q3_K: *blk = 256; *bytes = 110; return 0;
+    case QREF_Q2_0: *blk = 64; *bytes = 18; return 0;  /* (the reference's own type, src/gguf.h:26, 69) */
     default: return -1;
   }
 }
@@ -156,6 +158,51 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
           o->q[32 * b + 16 + i] = (int16_t)(type == QREF_Q4_0 ? hi - 8 : k_iq4nl[hi]);
         }
       }
+      return 0;
+    }
+    case QREF_Q2_0: {
+      /* src/quants.h:540-548 (dequant_row): 4 blocks of 64 (f16 d, 16 bytes: element j = bits 2 (j % 4) of byte j / 4),
+       * value (q - 1) * d */
+      for (int g = 0; g < 4; ++g) {
+        const uint8_t* blk = p + 18 * g;
+        o->d8[2 * g] = o->d8[2 * g + 1] = qref_fp16_to_f32(rd16(blk));
+        o->sc[2 * g] = o->sc[2 * g + 1] = 1;
+        for (int j = 0; j < 64; ++j) o->q[64 * g + j] = (int16_t)(((blk[2 + j / 4] >> (2 * (j % 4))) & 3) - 1);
+      }
+      return 0;
+    }
+    case QREF_Q3_K: {
+      /* src/quants.h:465-494 (dequant_q3_k, llama.cpp's order): hmask[32] | qs[64] | scales[12] | d. The 12 scale bytes
+       * unpack to 16 6-bit scales through the kmask shuffle; per 128 elements n and 2-bit shift j: 16 elements from
+       * q[l] and 16 from q[l + 16] (l < 16), value ((q >> shift) & 3) - (hmask & m ? 0 : 4), m = 1 << (4 n + j), the
+       * scales taken in order */
+      const uint8_t *hm = p, *q = p + 32;
+      o->d = qref_fp16_to_f32(rd16(p + 108));
+      uint32_t aux[4];
+      memcpy(aux, p + 96, 12);
+      const uint32_t kmask1 = 0x03030303u, kmask2 = 0x0f0f0f0fu, tmp = aux[2];
+      aux[2] = ((aux[0] >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4);
+      aux[3] = ((aux[1] >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4);
+      aux[0] = (aux[0] & kmask2) | (((tmp >> 0) & kmask1) << 4);
+      aux[1] = (aux[1] & kmask2) | (((tmp >> 2) & kmask1) << 4);
+      const int8_t* scales = (const int8_t*)aux;
+      int is = 0, e = 0;
+      unsigned m = 1;
+      for (int n = 0; n < 256; n += 128) {
+        int shift = 0;
+        for (int j = 0; j < 4; ++j) {
+          o->sc16[is] = scales[is] - 32;
+          ++is;
+          for (int l = 0; l < 16; ++l) o->q[e++] = (int16_t)(((q[l] >> shift) & 3) - ((hm[l] & m) ? 0 : 4));
+          o->sc16[is] = scales[is] - 32;
+          ++is;
+          for (int l = 0; l < 16; ++l) o->q[e++] = (int16_t)(((q[l + 16] >> shift) & 3) - ((hm[l + 16] & m) ? 0 : 4));
+          shift += 2;
+          m <<= 1;
+        }
+        q += 32;
+      }
+      for (int b = 0; b < 8; ++b) o->sc[b] = o->sc16[2 * b];  /* (per-32 view: the first half's scale) */
       return 0;
     }
     case QREF_Q8_0: {
@@ -285,7 +332,7 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
 
 int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
   const int r = decode_sb_raw(type, p, o);
-  if (r == 0 && type != QREF_Q6_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
+  if (r == 0 && type != QREF_Q6_K && type != QREF_Q3_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
     for (int i = 0; i < 16; ++i) o->sc16[i] = o->sc[i / 2];
   return r;
 }
@@ -298,7 +345,10 @@ static float dequant_value(int type, const qref_sb* o, int e) {
     case QREF_Q8_0:
     case QREF_Q4_0:
     case QREF_IQ4_NL: return o->d8[e / 32] * (float)o->q[e];
+    case QREF_Q2_0: return o->d8[e / 32] * (float)o->q[e];  /* (d * (float)(q - 1), src/quants.h:546) */
     case QREF_Q6_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
+    /* (Q3_K: dl * q with dl = d_all * (scale - 32), src/quants.h:486-489) */
+    case QREF_Q3_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
     /* (the IQ types: o.wd * o.wsc[e / 16] * (o.q[e] - o.qoff) - 0 with qoff = 0, src/quants.h:322) */
     default: return o->d * (float)o->sc16[e / 16] * (float)o->q[e] - 0.0f;
   }
@@ -354,7 +404,7 @@ static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
     for (int i = 0; i < 16; ++i) r->sc[s * 16 + i] = o.sc16[i];
     for (int b = 0; b < 8; ++b) {
       r->mn[s * 8 + b] = o.mn[b];
-      r->d[s * 8 + b] = (type == QREF_Q8_0 || type == QREF_Q4_0 || type == QREF_IQ4_NL) ? o.d8[b] : o.d;
+      r->d[s * 8 + b] = (type == QREF_Q8_0 || type == QREF_Q4_0 || type == QREF_IQ4_NL || type == QREF_Q2_0) ? o.d8[b] : o.d;
       r->dmin[s * 8 + b] = o.dmin;
     }
   }

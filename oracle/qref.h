@@ -19,7 +19,8 @@ extern "C" {
 
 /* GGML type ids (src/gguf.h:20-27) */
 enum { QREF_Q4_0 = 2, QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q5_K = 13, QREF_Q6_K = 14, QREF_IQ2_XXS = 16,
-       QREF_IQ2_XS = 17, QREF_IQ3_XXS = 18, QREF_IQ4_NL = 20, QREF_IQ3_S = 21, QREF_IQ2_S = 22, QREF_IQ4_XS = 23 };
+       QREF_IQ2_XS = 17, QREF_IQ3_XXS = 18, QREF_IQ4_NL = 20, QREF_IQ3_S = 21, QREF_IQ2_S = 22, QREF_IQ4_XS = 23,
+       QREF_Q3_K = 11, QREF_Q2_0 = 42 };
 
 /* A decoded 256-element superblock: integer quants plus the per-type scales.
  *   Q8_0:   w[e] = d8[e/32] * q[e]
@@ -33,8 +34,10 @@ enum { QREF_Q4_0 = 2, QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q5_K = 13, QREF_Q6_K =
  *   IQ2_XXS, IQ2_XS, IQ2_S: w[e] = d * sc16[e/16] * q[e]  (d = f16 d / 8, sc = 1 + 2 * 4-bit scale per 32 (XXS) or
  *           per 16 (XS, S), q = +-grid byte)
  *   IQ3_XXS: w[e] = d * sc[e/32] * q[e]   (d = f16 d / 4, sc = 1 + 2 * 4-bit scale, q = +-grid byte)
+ *   Q3_K:   w[e] = d * sc16[e/16] * q[e]  (sc16 = 6-bit scale - 32 per 16, q = 2-bit value - (hmask bit ? 0 : 4))
+ *   Q2_0:   w[e] = d8[e/32] * q[e]        (blocks of 64: one f16 d, q = 2-bit code - 1; d8 of both halves = d)
  * sc16[i] is the integer scale of elements 16i..16i+15 for every type (sc16[2b] = sc16[2b+1] = sc[b] except Q6_K,
- * IQ2_XS and IQ2_S, whose scales are per 16). */
+ * Q3_K, IQ2_XS and IQ2_S, whose scales are per 16). */
 typedef struct {
   float d, dmin;
   float d8[8];

@@ -153,3 +153,39 @@ def enc_iq3_xxs(d, scale_nib, gidx, sgn7):
     qs = np.asarray(gidx, dtype=np.uint8)
     ss = [_u32(sum(int(sgn7[4 * ib + l]) << (7 * l) for l in range(4)) | (int(scale_nib[ib]) << 28)) for ib in range(8)]
     return np.concatenate([_h(d), qs] + ss)
+
+
+# ---- Q3_K (ggml-common.h block_q3_K {hmask[32]; qs[64]; scales[12]; d}) and the reference's Q2_0 (src/gguf.h:26:
+# blocks of 64, f16 d then 16 bytes of 2-bit codes)
+def enc_q3_k(d, sc6, q):
+    """sc6: 16 scales 0..63 (stored; the value is sc6 - 32), q: 256 values -4..3 -> 110 bytes. Packed as ggml's
+    quantizer writes them: L = q + 4; element j's high bit (L > 3) in hmask[j % 32] bit j / 32 and its low 2 bits in
+    qs[32 (j / 128) + j % 32], bits 2 ((j % 128) / 32); scale j: low nibble in scales[j % 8] (nibble j / 8), top 2
+    bits in scales[8 + j % 4] (bits 2 (j / 4))."""
+    L = np.asarray(q, dtype=np.int64) + 4
+    hmask = np.zeros(32, dtype=np.uint8)
+    qs = np.zeros(64, dtype=np.uint8)
+    for j in range(256):
+        if L[j] > 3:
+            hmask[j % 32] |= 1 << (j // 32)
+        qs[32 * (j // 128) + j % 32] |= (int(L[j]) & 3) << (2 * ((j % 128) // 32))
+    scales = np.zeros(12, dtype=np.uint8)
+    for j in range(16):
+        ls = int(sc6[j])
+        if j < 8:
+            scales[j] = ls & 0xF
+        else:
+            scales[j - 8] |= (ls & 0xF) << 4
+        scales[8 + j % 4] |= (ls >> 4) << (2 * (j // 4))
+    return np.concatenate([hmask, qs, scales, _h(d)])
+
+
+def enc_q2_0(d4, codes):
+    """d4: 4 floats (one per 64), codes: 256 ints 0..3 -> 4 blocks of (f16 d, 16 bytes: element j in bits 2 (j % 4) of
+    byte j / 4)."""
+    out = bytearray()
+    for g in range(4):
+        out += _h(d4[g]).tobytes()
+        c = [int(v) for v in codes[64 * g:64 * g + 64]]
+        out += bytes(c[4 * t] | (c[4 * t + 1] << 2) | (c[4 * t + 2] << 4) | (c[4 * t + 3] << 6) for t in range(16))
+    return np.frombuffer(bytes(out), dtype=np.uint8)

@@ -295,6 +295,10 @@ def test_moe_decode_graph_replays(qm, dev, T):
     ((F.Q6_K, F.IQ2_S, F.IQ4_XS), 8, 256, 512, 3, 2), ((F.Q6_K, F.IQ2_S, F.IQ4_XS), 8, 256, 512, 64, 2),
     ((F.IQ4_XS,) * 3, 32, 4096, 512, 1, 8), ((F.IQ4_XS,) * 3, 16, 5120, 256, 4, 4),
     ((F.IQ4_XS,) * 3, 8, 512, 4096, 2, 4), ((F.IQ4_XS, F.IQ4_XS, F.Q6_K), 8, 512, 4096, 2, 4),
+    # Q3_K (per-16 scales) and the reference's Q2_0, alone and mixed (zero/engine_moe.h:297-300)
+    ((F.Q3_K,) * 3, 8, 512, 256, 1, 8), ((F.Q3_K,) * 3, 8, 512, 512, 40, 4), ((F.Q2_0,) * 3, 8, 512, 256, 3, 4),
+    ((F.Q2_0,) * 3, 16, 512, 512, 48, 4), ((F.Q2_0, F.Q2_0, F.Q3_K), 8, 256, 512, 2, 4),
+    ((F.Q3_K, F.IQ4_XS, F.Q2_0), 8, 512, 256, 40, 2),
 ])
 def test_moe_expert_types_and_mixes(qm, dev, types, NE, E, Fd, T, NU):
     import torch

@@ -1,6 +1,6 @@
 """Rows that are not whole superblocks, and the prompt GEMM with a caller-owned workspace.
 
-Q8_0, Q4_0 and IQ4_NL rows of K % 32 == 0 are padded at preparation with zero blocks to K rounded up to 256, as the
+Q8_0, Q4_0 and IQ4_NL rows of K % 32 == 0 (Q2_0: K % 64 == 0) are padded at preparation with zero blocks to K rounded up to 256, as the
 reference's load_w_pad / pad_small_block_rows (zero/engine.h:2102-2116; src/quants.h:581-595). The oracle computes on
 the explicitly padded GGUF rows (F.pad_small_rows) and activations of the padded length whose tail is zero -- the
 reference's own arithmetic on its padded weights. The MoE case is Flash Next's expert width 640 (down projection read
@@ -16,7 +16,7 @@ from tests.test_gpu_parity import TOL_INT8_PATH, acts, assert_elementwise, rel_e
 
 pytestmark = pytest.mark.gpu
 
-SMALL = [F.Q8_0, F.Q4_0, F.IQ4_NL]
+SMALL = [F.Q8_0, F.Q4_0, F.IQ4_NL, F.Q2_0]
 
 
 def padded_acts(M, K, seed):
@@ -30,6 +30,8 @@ def padded_acts(M, K, seed):
 @pytest.mark.parametrize("N,K,M", [(64, 640, 1), (48, 640, 3), (32, 96, 8), (144, 640, 40), (128, 1312, 130)])
 def test_padded_rows_gemv_and_gemm(qm, dev, qtype, N, K, M):
     import torch
+    if K % F.small_block(qtype):
+        pytest.skip("Q2_0 rows are whole 64-element blocks")
     Kp = F.padded_k(K)
     W = F.synth_weight(qtype, N, K, seed=qtype * 7 + K + M)
     assert W.shape[1] == F.row_bytes(qtype, K)
@@ -52,7 +54,7 @@ def test_padded_rows_gemv_and_gemm(qm, dev, qtype, N, K, M):
 
 
 @pytest.mark.parametrize("T,NU", [(2, 4), (40, 4)])  # decode-size experts, and the slot-tile path
-@pytest.mark.parametrize("td", [F.Q8_0, F.IQ4_NL])
+@pytest.mark.parametrize("td", [F.Q8_0, F.IQ4_NL, F.Q2_0])
 def test_moe_padded_expert_width(qm, dev, T, NU, td):
     """Experts of width Fv = 640: gate / up IQ4_XS with 640 rows per expert, down of 640-long rows padded to 768."""
     import torch

@@ -133,7 +133,7 @@ def test_iq3_s_decoder_round_trip():
 
 
 @pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S, F.IQ2_XXS,
-                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS])
+                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0])
 def test_synth_weights_have_the_requested_statistics(qtype):
     W = F.synth_weight(qtype, 64, 512, seed=5)
     assert W.shape == (64, F.row_bytes(qtype, 512))
@@ -278,3 +278,49 @@ def test_iq2_iq3xxs_decoder_round_trip(qtype):
         w = oracle.dequant_rows(qtype, raw[None], 256)[0]
         ref = (dd * sc16[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32)).astype(np.float32)
         assert np.array_equal(w, ref)
+
+
+def test_q3_k_decoder_round_trip_and_closed_form():
+    """The oracle's Q3_K decode (src/quants.h:465-494, the 12 scale bytes unpacked through the kmask shuffle) against
+    ggml's packing (tests/encoders.py), plus a closed form: block ib's values all ib - 4 with scales 32 + 2i + 1."""
+    rng = np.random.default_rng(11)
+    for it in range(40):
+        d = np.float16(rng.standard_normal())
+        sc6 = rng.integers(0, 64, 16)
+        q = rng.integers(-4, 4, 256)
+        if it == 0:
+            q = np.repeat(np.arange(8) - 4, 32)
+            sc6 = 32 + 2 * np.arange(16) + 1
+        if it == 1:
+            q[:] = -4
+            sc6[:] = 0
+        raw = enc.enc_q3_k(d, sc6, q)
+        assert raw.size == 110
+        o = oracle.decode_sb(F.Q3_K, raw)
+        assert np.array_equal(o["q"], q) and np.array_equal(o["sc16"], sc6 - 32) and o["d"] == np.float32(d)
+        w = oracle.dequant_rows(F.Q3_K, raw[None], 256)[0]
+        ref = np.float32(d) * (sc6 - 32)[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32)
+        assert np.array_equal(w, ref.astype(np.float32))
+        if it == 0:  # element 32 ib + e: d * (33 + 2 (2 ib + e // 16) - 32) * (ib - 4)
+            e = np.arange(256)
+            assert np.array_equal(w, (np.float32(d) * (1 + 2 * (e // 16)).astype(np.float32)
+                                      * (e // 32 - 4).astype(np.float32)).astype(np.float32))
+
+
+def test_q2_0_decoder_round_trip_and_closed_form():
+    """Q2_0 (the reference's 64-element blocks, value (code - 1) d, src/quants.h:540-548): random codes round trip,
+    and the byte 0xE4 (codes 0, 1, 2, 3 from bit 0 up) decodes to -1, 0, 1, 2 for every four elements."""
+    rng = np.random.default_rng(12)
+    for it in range(30):
+        d4 = (rng.standard_normal(4) * 0.1).astype(np.float16).astype(np.float32)
+        codes = rng.integers(0, 4, 256)
+        if it == 0:
+            codes = np.tile(np.arange(4), 64)
+        raw = enc.enc_q2_0(d4, codes)
+        if it == 0:
+            assert np.all(raw.reshape(4, 18)[:, 2:] == 0xE4)
+        o = oracle.decode_sb(F.Q2_0, raw)
+        assert np.array_equal(o["q"], codes - 1) and np.array_equal(o["d8"], np.repeat(d4, 2))
+        w = oracle.dequant_rows(F.Q2_0, raw[None], 256)[0]
+        assert np.array_equal(w, (np.repeat(d4, 64) * (codes - 1).astype(np.float32)).astype(np.float32))
+    assert F.row_bytes(F.Q2_0, 640) == 10 * 18 and F.row_bytes(F.Q3_K, 512) == 220
