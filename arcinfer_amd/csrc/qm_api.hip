@@ -37,7 +37,7 @@ int hip_fail(hipError_t e, const char* what) {
 bool known_type(int t) {
   return t == QM_Q4_0 || t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q5_K || t == QM_Q6_K || t == QM_IQ4_NL || t == QM_IQ3_S ||
          t == QM_IQ4_XS || t == QM_IQ2_XXS || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_IQ3_XXS || t == QM_Q3_K ||
-         t == QM_Q2_0;
+         t == QM_Q2_0 || t == QM_Q2_K;
 }
 
 int payload_bytes(int t) {
@@ -46,14 +46,14 @@ int payload_bytes(int t) {
     case QM_Q6_K: return 24;
     case QM_Q5_K: return 20;
     case QM_IQ3_S: case QM_IQ3_XXS: case QM_Q3_K: return 12;
-    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: case QM_Q2_0: return 8;
+    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: case QM_Q2_0: case QM_Q2_K: return 8;
     default: return 16;
   }
 }
 int header_bytes(int t) {
   switch (t) {
     case QM_IQ4_XS: case QM_Q2_0: return 8;
-    case QM_Q6_K: case QM_IQ2_S: case QM_Q3_K: return 20;
+    case QM_Q6_K: case QM_IQ2_S: case QM_Q3_K: case QM_Q2_K: return 20;
     case QM_IQ2_XS: return 12;
     case QM_IQ2_XXS: case QM_IQ3_XXS: return 4;
     default: return 16;
@@ -169,6 +169,7 @@ size_t qmatmul_sb_bytes(int type) {
     case QM_IQ3_XXS: return 98;
     case QM_Q3_K: return 110;
     case QM_Q2_0: return 72;
+    case QM_Q2_K: return 84;
     default: return 0;
   }
 }
@@ -340,8 +341,8 @@ int qmatmul_add_norm_quant(float* x, const float* t, const float* w, int K, floa
 static int check_acts(const char* fn, const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum,
                       int rows_needed, int M_stride) {
   if (!w || !aq || !asc) return fail(QM_ERR_ARG, "%s: null pointer", fn);
-  if ((w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K) && !absum)
-    return fail(QM_ERR_ARG, "%s: Q4_K, Q5_K and Q6_K need the per-16 activation sums", fn);
+  if ((w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q6_K || w->type == QM_Q2_K) && !absum)
+    return fail(QM_ERR_ARG, "%s: Q4_K, Q5_K, Q6_K and Q2_K need the per-16 activation sums", fn);
   if (rows_needed < 1 || M_stride < rows_needed)
     return fail(QM_ERR_SHAPE, "%s: %d activation rows with M_stride %d", fn, rows_needed, M_stride);
   if (!aligned(aq, 16)) return fail(QM_ERR_ARG, "%s: aq must be 16-byte aligned", fn);
@@ -376,7 +377,7 @@ int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* 
                            int32_t* isum, int32_t* msum, void* stream) {
   static const float unused = 0.0f;  // (the block-sum mode reads no scales)
   if (int st = check_acts("qmatmul_gemv_blocksums", w, aq, &unused, absum, T, M_stride)) return st;
-  if (!isum || ((w->type == QM_Q4_K || w->type == QM_Q5_K) && !msum))
+  if (!isum || ((w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q2_K) && !msum))
     return fail(QM_ERR_ARG, "qmatmul_gemv_blocksums: null output");
   if (T < 1 || T > 8) return fail(QM_ERR_SHAPE, "qmatmul_gemv_blocksums: T = %d", T);
   QM_CHECK_INIT();
@@ -545,9 +546,9 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
   if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
   for (const qm_weight* w : {gate, up, down})
-    if (w->type == QM_Q4_K || w->type == QM_Q5_K)
+    if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q2_K)
       return fail(QM_ERR_TYPE,
-                  "qmatmul_moe_grouped: Q4_K and Q5_K expert weights (per-block mins) are not supported, as in the "
+                  "qmatmul_moe_grouped: Q4_K, Q5_K and Q2_K expert weights (per-block mins) are not supported, as in the "
                   "reference's expert GEMMs (zero/engine_moe.h:284-301)");
   if (NE < 1 || NE > 1024 || NU < 1 || NU > NE || NU > 64 || T < 1 || M_stride < T || ldl < NE)
     return fail(QM_ERR_SHAPE, "qmatmul_moe_grouped: NE %d, NU %d, T %d, M_stride %d, ldl %d", NE, NU, T, M_stride, ldl);

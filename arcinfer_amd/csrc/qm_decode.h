@@ -42,10 +42,15 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
   } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
     r.q0 = ld_stream16(qp);
     r.h.x = ((const uint16_t*)hp)[b & 7];
-  } else if constexpr (TYPE == T_Q2_0) {
+  } else if constexpr (TYPE == T_Q2_0 || TYPE == T_Q2_K) {
     const uint32_t* q = (const uint32_t*)qp;
     r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), 0u, 0u};
-    r.h.x = ((const uint16_t*)hp)[block_scale_slot<TYPE>(b & 7)];
+    if constexpr (TYPE == T_Q2_0) {
+      r.h.x = ((const uint16_t*)hp)[block_scale_slot<TYPE>(b & 7)];
+    } else {
+      r.h.x = *(const uint32_t*)hp;                  // d, dmin
+      r.h.y = ((const uint16_t*)(hp + 4))[b & 7];   // the block's two scale / min bytes
+    }
   } else if constexpr (TYPE == T_Q3_K) {
     const uint32_t* q = (const uint32_t*)qp;
     r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2),
@@ -112,8 +117,9 @@ __device__ __forceinline__ uint64_t shr64_4(uint64_t x) {
 }
 
 // Decodes a loaded 32-block (index ib = b % 8 in its superblock): w[k] = elements 4k..4k+3 (int8x4), the integer
-// scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K, IQ2_XS and IQ2_S), the min mn, the float scales d (and dmin). Q6_K's
-// values come out as the stored 6-bit numbers 0..63 (the offset of 32 is removed by block_product).
+// scales sc (elements 0-15) and sc1 (16-31; = sc except Q6_K, Q3_K, Q2_K, IQ2_XS and IQ2_S), the min mn (Q2_K: the
+// first half's min | the second's << 16), the float scales d (and dmin). Q6_K's values come out as the stored 6-bit
+// numbers 0..63 (the offset of 32 is removed by block_product).
 template <int TYPE>
 __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename LdsFor<TYPE>::type* lds, int ib,
                                                const KvTab& kv, uint32_t wd[8], int& sc, int& sc1, int& mn,
@@ -141,6 +147,17 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     sc = (int)(int8_t)(r.h.x & 0xFFu);
     sc1 = (int)(int8_t)((r.h.x >> 8) & 0xFFu);
     d = h2f(r.h.y);
+    return;
+  }
+  if constexpr (TYPE == T_Q2_K) {
+    // values 0..3 as stored; per 16: scale (low nibble) and min (high nibble); mn holds both halves' mins
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wd[k] = ((k < 4 ? r.q0.x : r.q0.y) >> (2 * (k & 3))) & 0x03030303u;
+    sc = (int)(r.h.y & 0xFu);
+    sc1 = (int)((r.h.y >> 8) & 0xFu);
+    mn = (int)((r.h.y >> 4) & 0xFu) | (int)(((r.h.y >> 12) & 0xFu) << 16);
+    d = h2f(r.h.x);
+    dmin = h2f(r.h.x >> 16);
     return;
   }
   if constexpr (TYPE == T_Q2_0) {
@@ -247,7 +264,8 @@ struct BlockInts {
 template <int TYPE>
 __device__ __forceinline__ void block_dot(const uint32_t wd[8], int sc, int sc1, int mn, const uint4& x0,
                                           const uint4& x1, int bs0, int bs1, int& iv, int& mv) {
-  mv = Traits<TYPE>::MINS ? __mul24(mn, bs0 + bs1) : 0;
+  if constexpr (kMin16<TYPE>) mv = __mul24(mn & 0xFFFF, bs0) + __mul24(mn >> 16, bs1);
+  else mv = Traits<TYPE>::MINS ? __mul24(mn, bs0 + bs1) : 0;
   if constexpr (!Traits<TYPE>::SC16 && !Traits<TYPE>::SPLIT) {
     // one integer scale per 32-block: a single chain of 8 dot products
     int sum = dot4(x0.x, wd[0], 0);

@@ -22,6 +22,8 @@
 //   Q3_K   QB 12: two words of 2-bit fields, then a word of high bits: word h (h = 0, 1), byte i, bits 2j..2j+1 = the
 //                 low 2 bits of element 4 (4h + j) + i; word 2, byte i, bit k = the high bit (GGUF hmask) of element
 //                 4k + i. Value = (low | high << 2) - 4            HB 20: int8 scales[16] (6-bit - 32), f16 d, 2 zero
+//   Q2_K   QB 8: two words of 2-bit values laid out as Q3_K's first two (values 0..3)
+//                 HB 20: f16 d, f16 dmin, GGUF scales[16] (per 16 elements: scale low nibble, min high nibble)
 //   Q2_0   QB 8: two words of 2-bit codes laid out as Q3_K's first two; value = code - 1
 //                 HB 8: the four 64-blocks' f16 d (a 32-block uses its 64-block's: half-block b -> scale b / 2)
 // (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
@@ -38,7 +40,7 @@ namespace qm {
 
 enum : int {
   T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17, T_IQ3_XXS = 18,
-  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_Q3_K = 11, T_Q2_0 = 42
+  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_Q2_K = 10, T_Q3_K = 11, T_Q2_0 = 42
 };
 
 template <int TYPE> struct Traits;
@@ -57,12 +59,15 @@ template <> struct Traits<T_IQ2_XXS> { static constexpr int QB = 8, HB = 4, GGUF
 template <> struct Traits<T_IQ2_XS> { static constexpr int QB = 8, HB = 12, GGUF_SB = 74; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_IQ2_S> { static constexpr int QB = 8, HB = 20, GGUF_SB = 82; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_IQ3_XXS> { static constexpr int QB = 12, HB = 4, GGUF_SB = 98; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_Q2_K> { static constexpr int QB = 8, HB = 20, GGUF_SB = 84; static constexpr bool MINS = true, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_Q3_K> { static constexpr int QB = 12, HB = 20, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_Q2_0> { static constexpr int QB = 8, HB = 8, GGUF_SB = 72; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
 // f16 scales per 32-block in the header (Q8_0's layout; Q2_0: one per 64-block), no integer sub-scales
 template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL || TYPE == T_Q2_0;
 // the header's f16 scale of 32-block b (0..7) for kBlockScales types: its index among the header's halfwords
 template <int TYPE> __host__ __device__ constexpr int block_scale_slot(int b) { return TYPE == T_Q2_0 ? b >> 1 : b; }
+// mins per 16 elements (two per 32-block; the other MINS types have one per 32-block)
+template <int TYPE> constexpr bool kMin16 = TYPE == T_Q2_K;
 // whether the kernels need the per-16 activation sums (absum)
 template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
 // the codebook types whose tables live in LDS

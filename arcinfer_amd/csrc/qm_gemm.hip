@@ -659,6 +659,9 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     } else if constexpr (TYPE == T_Q3_K) {  // (the block's two words of 2-bit fields and its word of high bits)
       nib = *(const uint2*)r;
       hw = make_uint2(*(const uint32_t*)(r + 8), 0u);
+    } else if constexpr (TYPE == T_Q2_K) {
+      nib = *(const uint2*)r;
+      hw = make_uint2(0u, 0u);
     } else {
       nib = *(const uint2*)r;
       hw = make_uint2(0u, 0u);
@@ -674,6 +677,9 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     if constexpr (TYPE == T_IQ2_XS) {
       sc = make_uint4(h[0], h[1], 0u, 0u);
       dd = h[2];
+    } else if constexpr (TYPE == T_Q2_K) {  // (d and dmin first, then the 16 scale / min bytes)
+      sc = make_uint4(h[1], h[2], h[3], h[4]);
+      dd = h[0];
     } else {
       sc = make_uint4(h[0], h[1], h[2], h[3]);
       dd = h[4];
@@ -700,15 +706,25 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     const int sn = s + 1 < nsb ? s + 1 : s;
     fetch(sn);
     const uint32_t scw[4] = {hsc.x, hsc.y, hsc.z, hsc.w};
-    const float d = (TYPE == T_Q6_K || TYPE == T_Q3_K) ? h2f(hd) : h2f(hd) * kIqDScale<TYPE>;
+    const float d = (TYPE == T_Q6_K || TYPE == T_Q3_K || TYPE == T_Q2_K) ? h2f(hd) : h2f(hd) * kIqDScale<TYPE>;
+    const float dmin = TYPE == T_Q2_K ? h2f(hd >> 16) : 0.0f;
     load_hdr(sn, hsc, hd);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       if (b == 4) store(cur ^ 1);
       // B operands: elements 8hf..8hf+7 of the block's first half (o0) and of its second half (o1), signed
       uint32_t w[4];
-      int sc0, sc1;
-      if constexpr (TYPE == T_Q6_K) {
+      int sc0, sc1, mn0 = 0, mn1 = 0;
+      if constexpr (TYPE == T_Q2_K) {
+        const uint32_t wd[4] = {2u * hf, 2u * hf + 1, 4u + 2 * hf, 5u + 2 * hf};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = ((wd[k] < 4 ? nib[b].x : nib[b].y) >> (2 * (wd[k] & 3))) & 0x03030303u;
+        const uint32_t sm = (scw[b >> 1] >> (16 * (b & 1))) & 0xFFFFu;
+        sc0 = (int)(sm & 0xFu);
+        mn0 = (int)((sm >> 4) & 0xFu);
+        sc1 = (int)((sm >> 8) & 0xFu);
+        mn1 = (int)(sm >> 12);
+      } else if constexpr (TYPE == T_Q6_K) {
         const uint32_t A2 = hf ? hw[b].x : hw[b].x << 4, B2 = hf ? hw[b].y : hw[b].y << 4;
         w[0] = (nib[b].x & 0x0F0F0F0Fu) | (A2 & 0x30303030u);
         w[1] = (nib[b].y & 0x0F0F0F0Fu) | ((A2 >> 2) & 0x30303030u);
@@ -757,6 +773,17 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
           for (int r = 0; r < 16; ++r) {
             acc[mt][r] = fmaf(sc[r], (float)d0[r], acc[mt][r]);
             acc[mt][r] = fmaf(sc[16 + r], (float)d1[r], acc[mt][r]);
+          }
+          if constexpr (kMin16<TYPE>) {
+            // the mins per 16: acc -= sum over the halves h of (asc * bsum_h)[token] * (dmin * mn_h)[row], one K = 2 f32
+            // outer product (lane half hf: half hf); bsum_h of the token row from its staged int8 values
+            const uint4 av = *(const uint4*)(L.a[cur] + (mt * 32 + lc) * A_STRIDE + 32 * b + 16 * hf);
+            int bs = dot4(av.x, 0x01010101u, 0);
+            bs = dot4(av.y, 0x01010101u, bs);
+            bs = dot4(av.z, 0x01010101u, bs);
+            bs = dot4(av.w, 0x01010101u, bs);
+            const float my_u = my_asc * (float)bs, my_t = -dmin * (float)(hf ? mn1 : mn0);
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(my_u, my_t, acc[mt], 0, 0, 0);
           }
 #pragma unroll
           for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(acc[mt][r]));
@@ -1014,6 +1041,7 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
   switch (type) {
     case T_Q6_K: return dispatch_s16<T_Q6_K>(mode, a, s);
     case T_Q3_K: return dispatch_s16<T_Q3_K>(mode, a, s);
+    case T_Q2_K: return mode == GEMM_DENSE ? dispatch_s16<T_Q2_K>(mode, a, s) : hipErrorInvalidValue;
     case T_IQ2_XS: return dispatch_s16<T_IQ2_XS>(mode, a, s);
     case T_IQ2_S: return dispatch_s16<T_IQ2_S>(mode, a, s);
     default: break;

@@ -21,6 +21,7 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_IQ3_XXS: return gemv_dispatch<T_IQ3_XXS>(a, s);
     case T_Q3_K: return gemv_dispatch<T_Q3_K>(a, s);
     case T_Q2_0: return gemv_dispatch<T_Q2_0>(a, s);
+    case T_Q2_K: return gemv_dispatch<T_Q2_K>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

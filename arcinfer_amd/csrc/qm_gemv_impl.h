@@ -340,10 +340,11 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
 template <int TYPE>
 constexpr int gemvs_max_tb(int ch) { return ch <= (TYPE == T_Q6_K ? 4 : kIq2<TYPE> ? 3 : 5) ? 8 : 4; }
 
-// LDS bytes of gemvs_kernel for TB tokens
-static size_t gemvs_lds(int type, int K, int TB) {
+// LDS bytes of gemvs_kernel for TB tokens (the per-16 sums for the types that read them: kNeedsBsum)
+template <int TYPE>
+static size_t gemvs_lds(int K, int TB) {
   const int nb = K / 32;
-  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? sizeof(int) * nb : 0));
+  return (size_t)TB * ((size_t)K + sizeof(float) * nb + (kNeedsBsum<TYPE> ? sizeof(int) * nb : 0));
 }
 
 template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = false, int PC = (LPR == 256 ? 3 : 2),
@@ -359,7 +360,7 @@ static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   // queried once, for this instantiation's largest K.
   static const int per_cu = [] {
     int n = 0;
-    const size_t lds_max = AREG ? 0 : gemvs_lds(TYPE, 32 * LPR * CH, TB);
+    const size_t lds_max = AREG ? 0 : gemvs_lds<TYPE>(32 * LPR * CH, TB);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, false, AREG, 256, SPLIT>, 256, lds_max) !=
             hipSuccess || n < 1)
       n = 1;
@@ -375,7 +376,7 @@ static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   const int wgs = min(per_cu * cus, (a0.w.rows + GPW - 1) / GPW);
   GemvArgs a = a0;
   a.split = SPLIT && wgs > cus && a.w.rows > 2 * wgs * GPW ? cus : 0;
-  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG, 256, SPLIT><<<wgs, 256, AREG ? 0 : gemvs_lds(TYPE, a.w.K, TB), s>>>(a);
+  gemvs_kernel<TYPE, LPR, CH, EXACT, TB, PF, DUMP, AREG, 256, SPLIT><<<wgs, 256, AREG ? 0 : gemvs_lds<TYPE>(a.w.K, TB), s>>>(a);
   return hipGetLastError();
 }
 
@@ -411,7 +412,7 @@ static hipError_t gemv_route(const GemvArgs& a, hipStream_t s) {
     // of tokens, each launch reading the weights once
     int tb = gemvs_max_tb<TYPE>(nb <= 256 ? (nb + 31) / 32 : (nb + 127) / 128);
     const size_t cap = 80 * 1024 - sizeof(typename LdsFor<TYPE>::type);  // (the codebook tables' static LDS)
-    while (tb > 1 && gemvs_lds(TYPE, a.w.K, tb) > cap) tb >>= 1;
+    while (tb > 1 && gemvs_lds<TYPE>(a.w.K, tb) > cap) tb >>= 1;
     for (int t0 = 0; t0 < a.T; t0 += tb) {
       GemvArgs c = a;
       c.T = min(tb, a.T - t0);

@@ -103,6 +103,23 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         }
       }
     }
+  } else if constexpr (TYPE == T_Q2_K) {
+    // scales[16] (scale low nibble, min high nibble, per 16) | qs[64] | d | dmin (src/quants.h:159-169; decode.cl:151-160):
+    // element e of 32-block ib has the value (qs[32 (ib / 4) + e] >> 2 (ib % 4)) & 3
+    const uint8_t* qs = p + 16;
+    for (int t = 0; t < 8 * Tr::QB; ++t) q[t] = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+      uint8_t* dst = q + Tr::QB * ib;
+      for (int e = 0; e < 32; ++e) {
+        const int v = (qs[32 * (ib >> 2) + e] >> (2 * (ib & 3))) & 3, k = e >> 2, i = e & 3;
+        dst[4 * (k >> 2) + i] |= (uint8_t)(v << (2 * (k & 3)));
+      }
+    }
+    h[0] = p[80];
+    h[1] = p[81];
+    h[2] = p[82];
+    h[3] = p[83];
+    for (int i = 0; i < 16; ++i) h[4 + i] = p[i];
   } else if constexpr (TYPE == T_Q3_K) {
     // hmask[32] | qs[64] | scales[12] | d (src/quants.h:465-494; decode.cl:162-176): element e of 32-block ib has the
     // low 2 bits (qs[32 (ib / 4) + e] >> 2 (ib % 4)) & 3 and the high bit (hmask[e] >> ib) & 1, value (low | high << 2)
@@ -214,6 +231,7 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, int kraw
     case T_IQ3_S: repack_kernel<T_IQ3_S><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q3_K: repack_kernel<T_Q3_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_Q2_K: repack_kernel<T_Q2_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q2_0: repack_kernel<T_Q2_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;

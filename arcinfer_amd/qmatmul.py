@@ -227,7 +227,7 @@ def gemv_blocksums(w, aq, absum, T=1, stream=None):
     import torch
     nb = w.K // 32
     isum = torch.empty((T, w.rows, nb), dtype=torch.int32, device=aq.device)
-    msum = torch.empty((T, w.rows, nb), dtype=torch.int32, device=aq.device) if w.qtype in (12, 13) else None
+    msum = torch.empty((T, w.rows, nb), dtype=torch.int32, device=aq.device) if w.qtype in (12, 13, 10) else None
     _call("qmatmul_gemv_blocksums", w.handle, _ptr(aq), _ptr(absum), aq.shape[0], T, _ptr(isum), _ptr(msum),
           _stream(stream))
     return isum, msum

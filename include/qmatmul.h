@@ -43,7 +43,8 @@ extern "C" {
 /* GGML type ids (src/gguf.h:20-27) of the weight types this path decodes */
 typedef enum {
   QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ2_XXS = 16, QM_IQ2_XS = 17,
-  QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23, QM_Q3_K = 11, QM_Q2_0 = 42
+  QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23, QM_Q2_K = 10, QM_Q3_K = 11,
+  QM_Q2_0 = 42
 } qm_type;
 
 typedef enum {
@@ -133,7 +134,7 @@ int qmatmul_add_norm_quant_ex(float* x, const float* t, const float* w, int K, f
 
 /* Decode GEMV, T tokens (1..8) against one read of the weight:
  *   C[t*ldc + c_off + n] (+)= sum_k W[n][k] * a_t[k],  t < T, n < rows(w)
- * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K, Q5_K and Q6_K.
+ * a_t = token t's int8 row of aq with its per-32 scales. accumulate 0 or 1. absum is required for Q4_K, Q5_K, Q6_K and Q2_K.
  * Replaces the gemv / gemv_v / gemv_mt / gemv_mt_v launches of Engine::matmul1 (zero/engine.h:3184-3232;
  * zero/kernels/decode.cl:636-737, 1074-1141, 1145-1411). */
 int qmatmul_gemv(const qm_weight* w, const int8_t* aq, const float* asc, const int16_t* absum, int M_stride, int T,
@@ -197,7 +198,7 @@ int qmatmul_moe_route(const float* logits, int ldl, int T, int NE, int NU, int* 
  * (token, expert) pairs to slots, expert-grouped int8 MFMA GEMMs over the slot tiles, and the combine in fixed
  * order (moe.cl:332-340); at decode sizes (T * NU <= 64) GEMV-shaped expert kernels instead. Gate, up and down each
  * have their own type, any of Q8_0, Q4_0, IQ4_NL, IQ4_XS, IQ3_S, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, Q6_K, Q3_K, Q2_0 --
- * the types of the reference's expert GEMM moe_rg (zero/engine_moe.h:297-306); types with per-block mins (Q4_K, Q5_K) return
+ * the types of the reference's expert GEMM moe_rg (zero/engine_moe.h:297-306); types with per-block mins (Q4_K, Q5_K, Q2_K) return
  * QM_ERR_TYPE, as there. accumulate 0 or 1.
  * ws: device workspace of at least qmatmul_moe_workspace_size bytes (layout: qmatmul_moe_ws_layout). */
 int qmatmul_moe_grouped(const qm_weight* gate, const qm_weight* up, const qm_weight* down, int NE, const float* logits,
@@ -231,7 +232,8 @@ int qmatmul_moe_ws_layout(int T, int NE, int NU, int E, int F, qm_moe_ws_layout*
 /* Verification hooks: the integer block sums of the GEMV / GEMM kernels, from the same decode and dot-product
  * code as the products. For each token m < M, row n and 32-block b (index (m*rows + n)*(K/32) + b):
  *   isum[...] = sc_b * sum_{k in b} q[n][k] * a_m[k]   (Q8_0: sc_b = 1)
- *   msum[...] = mn_b * (absum of the block's two 16-halves)   (Q4_K only; NULL otherwise)
+ *   msum[...] = mn_b * (absum of the block's two 16-halves)   (Q4_K, Q5_K; Q2_K: mn0 * bs0 + mn1 * bs1 with its
+ *               mins per 16; NULL otherwise)
  * These are the reference's `sc0 * lo + sc1 * hi` and `mn0 * bs0 + mn1 * bs1` (zero/kernels/decode.cl:695-706). */
 int qmatmul_gemv_blocksums(const qm_weight* w, const int8_t* aq, const int16_t* absum, int M_stride, int T,
                            int32_t* isum, int32_t* msum, void* stream);

@@ -78,7 +78,7 @@ def _p(a):
 class SB(ctypes.Structure):
     _fields_ = [("d", ctypes.c_float), ("dmin", ctypes.c_float), ("d8", ctypes.c_float * 8),
                 ("sc", ctypes.c_int * 8), ("mn", ctypes.c_int * 8), ("q", ctypes.c_int16 * 256),
-                ("sc16", ctypes.c_int * 16)]
+                ("sc16", ctypes.c_int * 16), ("mn16", ctypes.c_int * 16)]
 
 
 def fp16_to_f32(h):
@@ -102,7 +102,8 @@ def decode_sb(qtype, sb):
     if lib().qref_decode_sb(qtype, _p(sb), ctypes.byref(o)):
         raise ValueError(f"decode_sb: type {qtype}")
     return {"d": o.d, "dmin": o.dmin, "d8": np.array(o.d8[:], np.float32), "sc": np.array(o.sc[:], np.int64),
-            "mn": np.array(o.mn[:], np.int64), "q": np.array(o.q[:], np.int64), "sc16": np.array(o.sc16[:], np.int64)}
+            "mn": np.array(o.mn[:], np.int64), "q": np.array(o.q[:], np.int64), "sc16": np.array(o.sc16[:], np.int64),
+            "mn16": np.array(o.mn16[:], np.int64)}
 
 
 def dequant_rows(qtype, W, K):

@@ -84,6 +84,7 @@ int qref_block_info(int type, int* blk, int* bytes) {
     case QREF_IQ2_S: *blk = 256; *bytes = 82; return 0;
     case QREF_IQ3_XXS: *blk = 256; *bytes = 98; return 0;
     case QREF_Q3_K: *blk = 256; *bytes = 110; return 0;
+    case QREF_Q2_K: *blk = 256; *bytes = 84; return 0;
     case QREF_Q2_0: *blk = 64; *bytes = 18; return 0;  /* (the reference's own type, src/gguf.h:26, 69) */
     default: return -1;
   }
@@ -168,6 +169,26 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
         o->d8[2 * g] = o->d8[2 * g + 1] = qref_fp16_to_f32(rd16(blk));
         o->sc[2 * g] = o->sc[2 * g + 1] = 1;
         for (int j = 0; j < 64; ++j) o->q[64 * g + j] = (int16_t)(((blk[2 + j / 4] >> (2 * (j % 4))) & 3) - 1);
+      }
+      return 0;
+    }
+    case QREF_Q2_K: {
+      /* src/quants.h:159-169: scales[16] (per 16 elements: scale = low nibble, min = high nibble) | qs[64] | d | dmin;
+       * element e (n = e / 128, j = (e % 128) / 32): q = (qs[32 n + e % 32] >> 2 j) & 3 */
+      const uint8_t *sc = p, *qs = p + 16;
+      o->d = qref_fp16_to_f32(rd16(p + 80));
+      o->dmin = qref_fp16_to_f32(rd16(p + 82));
+      for (int i = 0; i < 16; ++i) {
+        o->sc16[i] = sc[i] & 0xF;
+        o->mn16[i] = sc[i] >> 4;
+      }
+      for (int e = 0; e < 256; ++e) {
+        const int n = e / 128, r = e % 128, j = r / 32;
+        o->q[e] = (int16_t)((qs[32 * n + r % 32] >> (2 * j)) & 3);
+      }
+      for (int b = 0; b < 8; ++b) {
+        o->sc[b] = o->sc16[2 * b];  /* (per-32 view: the first half's scale and min) */
+        o->mn[b] = o->mn16[2 * b];
       }
       return 0;
     }
@@ -332,8 +353,10 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
 
 int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
   const int r = decode_sb_raw(type, p, o);
-  if (r == 0 && type != QREF_Q6_K && type != QREF_Q3_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
+  if (r == 0 && type != QREF_Q6_K && type != QREF_Q3_K && type != QREF_Q2_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
     for (int i = 0; i < 16; ++i) o->sc16[i] = o->sc[i / 2];
+  if (r == 0 && type != QREF_Q2_K)
+    for (int i = 0; i < 16; ++i) o->mn16[i] = o->mn[i / 2];
   return r;
 }
 
@@ -349,6 +372,8 @@ static float dequant_value(int type, const qref_sb* o, int e) {
     case QREF_Q6_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
     /* (Q3_K: dl * q with dl = d_all * (scale - 32), src/quants.h:486-489) */
     case QREF_Q3_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e];
+    /* (Q2_K: wd * wsc * q - wdmin * wmn per 16, src/quants.h:322) */
+    case QREF_Q2_K: return o->d * (float)o->sc16[e / 16] * (float)o->q[e] - o->dmin * (float)o->mn16[e / 16];
     /* (the IQ types: o.wd * o.wsc[e / 16] * (o.q[e] - o.qoff) - 0 with qoff = 0, src/quants.h:322) */
     default: return o->d * (float)o->sc16[e / 16] * (float)o->q[e] - 0.0f;
   }
@@ -390,7 +415,7 @@ void qref_quantize_act(const float* x, int M, int K, int M_stride, int act32, in
 typedef struct {
   int8_t* q;   /* [K] */
   int* sc;     /* [K/16]: integer scale of each 16-element half-block */
-  int* mn;     /* [K/32] */
+  int* mn;     /* [K/16]: min of each 16-element half-block */
   float* d;    /* [K/32]: d of the block's superblock (Q8_0: the block's own scale) */
   float* dmin; /* [K/32] */
 } row_dec;
@@ -403,7 +428,8 @@ static void decode_row(int type, const uint8_t* row, int K, row_dec* r) {
     for (int e = 0; e < 256; ++e) r->q[s * 256 + e] = (int8_t)o.q[e];
     for (int i = 0; i < 16; ++i) r->sc[s * 16 + i] = o.sc16[i];
     for (int b = 0; b < 8; ++b) {
-      r->mn[s * 8 + b] = o.mn[b];
+      r->mn[s * 16 + 2 * b] = o.mn16[2 * b];
+      r->mn[s * 16 + 2 * b + 1] = o.mn16[2 * b + 1];
       r->d[s * 8 + b] = (type == QREF_Q8_0 || type == QREF_Q4_0 || type == QREF_IQ4_NL || type == QREF_Q2_0) ? o.d8[b] : o.d;
       r->dmin[s * 8 + b] = o.dmin;
     }
@@ -423,9 +449,10 @@ static double row_dot(int type, const row_dec* r, int K, const int8_t* a, const 
     const int iv = r->sc[2 * b] * lo + r->sc[2 * b + 1] * hi;
     const float sa = asc[(size_t)b * M_stride + m];
     float v;
-    if (type == QREF_Q4_K || type == QREF_Q5_K) {
-      const int bs = (int)absum[(size_t)(2 * b) * M_stride + m] + (int)absum[(size_t)(2 * b + 1) * M_stride + m];
-      const int mv = r->mn[b] * bs;
+    if (type == QREF_Q4_K || type == QREF_Q5_K || type == QREF_Q2_K) {
+      /* (mn0 * bs0 + mn1 * bs1, decode.cl:703-706; one min per 32 for Q4_K / Q5_K) */
+      const int bs0 = absum[(size_t)(2 * b) * M_stride + m], bs1 = absum[(size_t)(2 * b + 1) * M_stride + m];
+      const int mv = r->mn[2 * b] * bs0 + r->mn[2 * b + 1] * bs1;
       v = sa * (r->d[b] * (float)iv - r->dmin[b] * (float)mv);
       if (msums) msums[b] = mv;
     } else {
@@ -452,7 +479,7 @@ int qref_blockdot(int type, const uint8_t* W, int N, int K, const int8_t* aq, co
     row_dec r;
     r.q = (int8_t*)malloc((size_t)K);
     r.sc = (int*)malloc(sizeof(int) * 2 * nb);
-    r.mn = (int*)malloc(sizeof(int) * nb);
+    r.mn = (int*)malloc(sizeof(int) * 2 * nb);
     r.d = (float*)malloc(sizeof(float) * nb);
     r.dmin = (float*)malloc(sizeof(float) * nb);
 #ifdef _OPENMP
@@ -549,7 +576,8 @@ int qref_moe_forward_ex(int type_gate, const uint8_t* Wg, int type_up, const uin
   /* (types with per-block mins need the activation sums, which the expert path does not carry: the reference's
    *  expert GEMMs take no min types either, zero/engine_moe.h:284-301) */
   if (type_gate == QREF_Q4_K || type_up == QREF_Q4_K || type_down == QREF_Q4_K || type_gate == QREF_Q5_K ||
-      type_up == QREF_Q5_K || type_down == QREF_Q5_K)
+      type_up == QREF_Q5_K || type_down == QREF_Q5_K || type_gate == QREF_Q2_K || type_up == QREF_Q2_K ||
+      type_down == QREF_Q2_K)
     return -1;
   if (sh && sh_gated && ldl < NE + 1) return -1;
   int* ids = (int*)malloc(sizeof(int) * (size_t)T * NU);
@@ -565,7 +593,7 @@ int qref_moe_forward_ex(int type_gate, const uint8_t* Wg, int type_up, const uin
     const int KM = E > F ? E : F;
     r.q = (int8_t*)malloc((size_t)KM);
     r.sc = (int*)malloc(sizeof(int) * KM / 16);
-    r.mn = (int*)malloc(sizeof(int) * KM / 32);
+    r.mn = (int*)malloc(sizeof(int) * KM / 16);
     r.d = (float*)malloc(sizeof(float) * KM / 32);
     r.dmin = (float*)malloc(sizeof(float) * KM / 32);
     float* h = (float*)malloc(sizeof(float) * F);

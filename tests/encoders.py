@@ -189,3 +189,14 @@ def enc_q2_0(d4, codes):
         c = [int(v) for v in codes[64 * g:64 * g + 64]]
         out += bytes(c[4 * t] | (c[4 * t + 1] << 2) | (c[4 * t + 2] << 4) | (c[4 * t + 3] << 6) for t in range(16))
     return np.frombuffer(bytes(out), dtype=np.uint8)
+
+
+def enc_q2_k(d, dmin, sc4, mn4, q):
+    """ggml block_q2_K {scales[16]; qs[64]; d; dmin}: sc4 / mn4 16 scales and mins 0..15 (per 16 elements, scale in
+    the low nibble), q 256 values 0..3: element 128n + 32j + l in qs[32n + l], bits 2j -> 84 bytes."""
+    scales = (np.asarray(sc4, dtype=np.int64) | (np.asarray(mn4, dtype=np.int64) << 4)).astype(np.uint8)
+    qs = np.zeros(64, dtype=np.uint8)
+    for e in range(256):
+        n, j, l = e // 128, (e % 128) // 32, e % 32
+        qs[32 * n + l] |= int(q[e]) << (2 * j)
+    return np.concatenate([scales, qs, _h(d), _h(dmin)])

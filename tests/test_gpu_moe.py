@@ -335,11 +335,14 @@ def test_moe_refuses_min_types_and_checks_the_gate_column(qm, dev):
     import torch
     NE, E, Fd, T, NU = 8, 256, 256, 2, 2
     s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=1)
-    Wk = F.synth_weight(F.Q4_K, NE * Fd, E, seed=2)
-    wk = qm.QWeight(F.Q4_K, to_dev(Wk, dev), NE * Fd, E)
-    with pytest.raises(qm.QMatmulError) as ei:
-        qm.moe_grouped(wk, s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
-    assert ei.value.status == 3  # QM_ERR_TYPE
+    for tk in (F.Q4_K, F.Q2_K):  # (per-block mins: no expert type, as the reference's)
+        Wk = F.synth_weight(tk, NE * Fd, E, seed=2)
+        wk = qm.QWeight(tk, to_dev(Wk, dev), NE * Fd, E)
+        with pytest.raises(qm.QMatmulError) as ei:
+            qm.moe_grouped(wk, s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"])
+        assert ei.value.status == 3  # QM_ERR_TYPE
+        if tk == F.Q4_K:
+            wk.release()
     sh = torch.zeros((T, E), device=dev)
     with pytest.raises(qm.QMatmulError) as ei:  # (logits have exactly NE columns: no gate logit)
         qm.moe_grouped(s["g"], s["u"], s["d"], NE, s["lgt"], NU, s["aq"], s["asc"], s["out"], s["ws"], sh=sh)

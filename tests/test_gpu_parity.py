@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 TOL_INT8_PATH = 1e-4
 TOL_F32_REF = 1e-3
 TYPES = [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S]
-GEMV_TYPES = TYPES + [F.Q6_K, F.Q5_K, F.Q4_0, F.IQ4_NL, F.IQ2_XXS, F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0]
+GEMV_TYPES = TYPES + [F.Q6_K, F.Q5_K, F.Q4_0, F.IQ4_NL, F.IQ2_XXS, F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0, F.Q2_K]
 
 
 def rel_err(got, ref):
@@ -91,7 +91,7 @@ def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
     _, risum, rmsum = oracle.blockdot(qtype, W, K, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=T,
                                       blocksums=True)
     assert np.array_equal(isum.cpu().numpy(), risum)
-    if qtype == F.Q4_K:
+    if msum is not None:  # (Q4_K, Q5_K, Q2_K)
         assert np.array_equal(msum.cpu().numpy(), rmsum)
 
 

@@ -324,3 +324,44 @@ def test_q2_0_decoder_round_trip_and_closed_form():
         w = oracle.dequant_rows(F.Q2_0, raw[None], 256)[0]
         assert np.array_equal(w, (np.repeat(d4, 64) * (codes - 1).astype(np.float32)).astype(np.float32))
     assert F.row_bytes(F.Q2_0, 640) == 10 * 18 and F.row_bytes(F.Q3_K, 512) == 220
+
+
+def test_q2_k_decoder_round_trip():
+    """Q2_K (src/quants.h:159-169: scale and min per 16 elements) against ggml's block struct (tests/encoders.py)."""
+    rng = np.random.default_rng(13)
+    for it in range(40):
+        d, dmin = np.float16(rng.random()), np.float16(rng.random())
+        sc4, mn4 = rng.integers(0, 16, 16), rng.integers(0, 16, 16)
+        q = rng.integers(0, 4, 256)
+        if it == 0:
+            q[:] = 3
+            sc4[:], mn4[:] = 15, 15
+        raw = enc.enc_q2_k(d, dmin, sc4, mn4, q)
+        assert raw.size == 84
+        o = oracle.decode_sb(F.Q2_K, raw)
+        assert np.array_equal(o["q"], q) and np.array_equal(o["sc16"], sc4) and np.array_equal(o["mn16"], mn4)
+        assert o["d"] == np.float32(d) and o["dmin"] == np.float32(dmin)
+        w = oracle.dequant_rows(F.Q2_K, raw[None], 256)[0]
+        e16 = np.arange(256) // 16
+        ref = (np.float32(d) * sc4[e16].astype(np.float32) * q.astype(np.float32)
+               - np.float32(dmin) * mn4[e16].astype(np.float32)).astype(np.float32)
+        assert np.array_equal(w, ref)
+
+
+def test_per16_mins_enter_the_block_dot():
+    """The block-dot oracle's Q2_K min term is mn0 * bs0 + mn1 * bs1 (decode.cl:703-706): with all values 0 the
+    block sums vanish and the product is -sa * dmin * (mn0 * bs0 + mn1 * bs1) per block, brute-forced here."""
+    rng = np.random.default_rng(14)
+    d, dmin = np.float16(0.5), np.float16(0.25)
+    mn4 = rng.integers(0, 16, 16)
+    raw = enc.enc_q2_k(d, dmin, rng.integers(0, 16, 16), mn4, np.zeros(256, np.int64))
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    aq, asc, absum = oracle.quantize_act(x)
+    C, isum, msum = oracle.blockdot(F.Q2_K, raw[None], 256, aq, asc, absum, blocksums=True)
+    assert np.all(isum == 0)
+    bs = absum[:, 0].astype(np.int64)
+    want_m = np.array([mn4[2 * b] * bs[2 * b] + mn4[2 * b + 1] * bs[2 * b + 1] for b in range(8)])
+    assert np.array_equal(msum.reshape(-1), want_m)
+    want = sum(float(np.float32(asc[b, 0]) * (np.float32(d) * np.float32(0) - np.float32(dmin) * np.float32(want_m[b])))
+               for b in range(8))
+    assert abs(float(C[0, 0]) - want) <= 1e-6 * max(1.0, abs(want))
