@@ -12,7 +12,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqmatmul.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HOST_SOURCES = ["qm_gguf.cpp"]  # host-only C++ (g++)
-SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemv_q8.hip", "qm_gemv_k.hip", "qm_gemv_q6.hip", "qm_gemv_iq.hip", "qm_gemv_iq2.hip", "qm_gemv_iq2s.hip", "qm_gemv_q3.hip", "qm_gemm.hip", "qm_gemm_f16.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
+SOURCES = ["qm_prep.hip", "qm_gemv.hip", "qm_gemv_q8.hip", "qm_gemv_k.hip", "qm_gemv_q6.hip", "qm_gemv_iq.hip", "qm_gemv_iq2.hip", "qm_gemv_iq2s.hip", "qm_gemv_q3.hip", "qm_gemv_iq1.hip", "qm_gemm.hip", "qm_gemm_f16.hip", "qm_moe.hip", "qm_moe_dec.hip", "qm_producers.hip", "qm_api.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt",

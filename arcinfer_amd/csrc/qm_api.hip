@@ -37,7 +37,7 @@ int hip_fail(hipError_t e, const char* what) {
 bool known_type(int t) {
   return t == QM_Q4_0 || t == QM_Q8_0 || t == QM_Q4_K || t == QM_Q5_K || t == QM_Q6_K || t == QM_IQ4_NL || t == QM_IQ3_S ||
          t == QM_IQ4_XS || t == QM_IQ2_XXS || t == QM_IQ2_XS || t == QM_IQ2_S || t == QM_IQ3_XXS || t == QM_Q3_K ||
-         t == QM_Q2_0 || t == QM_Q2_K;
+         t == QM_Q2_0 || t == QM_Q2_K || t == QM_IQ1_S || t == QM_IQ1_M;
 }
 
 int payload_bytes(int t) {
@@ -46,7 +46,7 @@ int payload_bytes(int t) {
     case QM_Q6_K: return 24;
     case QM_Q5_K: return 20;
     case QM_IQ3_S: case QM_IQ3_XXS: case QM_Q3_K: return 12;
-    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: case QM_Q2_0: case QM_Q2_K: return 8;
+    case QM_IQ2_XXS: case QM_IQ2_XS: case QM_IQ2_S: case QM_Q2_0: case QM_Q2_K: case QM_IQ1_S: case QM_IQ1_M: return 8;
     default: return 16;
   }
 }
@@ -55,7 +55,7 @@ int header_bytes(int t) {
     case QM_IQ4_XS: case QM_Q2_0: return 8;
     case QM_Q6_K: case QM_IQ2_S: case QM_Q3_K: case QM_Q2_K: return 20;
     case QM_IQ2_XS: return 12;
-    case QM_IQ2_XXS: case QM_IQ3_XXS: return 4;
+    case QM_IQ2_XXS: case QM_IQ3_XXS: case QM_IQ1_S: case QM_IQ1_M: return 4;
     default: return 16;
   }
 }
@@ -170,6 +170,8 @@ size_t qmatmul_sb_bytes(int type) {
     case QM_Q3_K: return 110;
     case QM_Q2_0: return 72;
     case QM_Q2_K: return 84;
+    case QM_IQ1_S: return 50;
+    case QM_IQ1_M: return 56;
     default: return 0;
   }
 }
@@ -545,6 +547,10 @@ int qmatmul_moe_grouped_ex(const qm_weight* gate, const qm_weight* up, const qm_
                            int accumulate, void* ws, size_t ws_bytes, void* stream) {
   if (!gate || !up || !down || !logits || !aq || !asc || !x || !ws)
     return fail(QM_ERR_ARG, "qmatmul_moe_grouped: null pointer");
+  for (const qm_weight* w : {gate, up, down})
+    if (w->type == QM_IQ1_S || w->type == QM_IQ1_M)
+      return fail(QM_ERR_TYPE, "qmatmul_moe_grouped: IQ1_S / IQ1_M are not expert types of the reference's moe_rg "
+                               "(zero/engine_moe.h:296-301)");
   for (const qm_weight* w : {gate, up, down})
     if (w->type == QM_Q4_K || w->type == QM_Q5_K || w->type == QM_Q2_K)
       return fail(QM_ERR_TYPE,

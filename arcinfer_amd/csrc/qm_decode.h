@@ -11,6 +11,8 @@ template <> struct LdsFor<T_IQ2_XXS> { using type = IqLds<T_IQ2_XXS>; };
 template <> struct LdsFor<T_IQ2_XS> { using type = IqLds<T_IQ2_XS>; };
 template <> struct LdsFor<T_IQ2_S> { using type = IqLds<T_IQ2_S>; };
 template <> struct LdsFor<T_IQ3_XXS> { using type = IqLds<T_IQ3_XXS>; };
+template <> struct LdsFor<T_IQ1_S> { using type = Iq1Lds; };
+template <> struct LdsFor<T_IQ1_M> { using type = Iq1Lds; };
 
 // Fills a work-group's LDS tables for TYPE (nothing for the types without codebooks in LDS); the caller
 // synchronizes before use.
@@ -18,6 +20,7 @@ template <int TYPE>
 __device__ __forceinline__ void lds_fill(typename LdsFor<TYPE>::type* t) {
   if constexpr (TYPE == T_IQ3_S) iq3_lds_fill(t);
   else if constexpr (kIq2<TYPE>) iq_lds_fill<TYPE>(t);
+  else if constexpr (kIq1<TYPE>) iq1_lds_fill(t);
 }
 
 // The raw bytes a lane needs for 32-block b of row n: payload (q0; Q8_0, Q5_K and Q6_K also q1) and header (h).
@@ -42,6 +45,10 @@ __device__ __forceinline__ RawBlk load_block_at(const uint8_t* qrow, const uint8
   } else if constexpr (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) {
     r.q0 = ld_stream16(qp);
     r.h.x = ((const uint16_t*)hp)[b & 7];
+  } else if constexpr (kIq1<TYPE>) {
+    const uint32_t* q = (const uint32_t*)qp;
+    r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), 0u, 0u};
+    r.h.x = *(const uint32_t*)hp;  // f16 d
   } else if constexpr (TYPE == T_Q2_0 || TYPE == T_Q2_K) {
     const uint32_t* q = (const uint32_t*)qp;
     r.q0 = u32x4_t{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), 0u, 0u};
@@ -147,6 +154,23 @@ __device__ __forceinline__ void decode_block32(const RawBlk& r, const typename L
     sc = (int)(int8_t)(r.h.x & 0xFFu);
     sc1 = (int)(int8_t)((r.h.x >> 8) & 0xFFu);
     d = h2f(r.h.y);
+    return;
+  }
+  if constexpr (kIq1<TYPE>) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      uint32_t idx;
+      bool neg;
+      iq1_index<TYPE>(r.q0.x, r.q0.y, l, idx, neg);
+      iq1_group(lds, idx, neg, wd[2 * l], wd[2 * l + 1]);
+    }
+    if constexpr (TYPE == T_IQ1_S) {
+      sc = sc1 = 2 * (int)((r.q0.y >> 12) & 7u) + 1;
+    } else {
+      sc = 2 * (int)((r.q0.y >> 16) & 7u) + 1;
+      sc1 = 2 * (int)((r.q0.y >> 19) & 7u) + 1;
+    }
+    d = h2f(r.h.x) * 0.125f;
     return;
   }
   if constexpr (TYPE == T_Q2_K) {

@@ -24,6 +24,11 @@
 //                 4k + i. Value = (low | high << 2) - 4            HB 20: int8 scales[16] (6-bit - 32), f16 d, 2 zero
 //   Q2_K   QB 8: two words of 2-bit values laid out as Q3_K's first two (values 0..3)
 //                 HB 20: f16 d, f16 dmin, GGUF scales[16] (per 16 elements: scale low nibble, min high nibble)
+//   IQ1_S  QB 8: the block's 4 grid index low bytes, then GGUF qh (u16: 3 high index bits per 8 elements, bits 12-14
+//                 the scale s, bit 15 the delta sign), 2 zero      HB 4: f16 d, 2 zero
+//   IQ1_M  QB 8: the block's 4 grid index low bytes, GGUF qh[2] (per 8 elements: 3 high index bits, delta sign), then
+//                 the block's two 3-bit scales (bits 0-2, 3-5)     HB 4: f16 d (assembled from the GGUF scale words), 2 zero
+//                 value = 8 * grid + delta (delta = -1 where the sign bit is set, else 1), w = d / 8 * (2 s + 1) * value
 //   Q2_0   QB 8: two words of 2-bit codes laid out as Q3_K's first two; value = code - 1
 //                 HB 8: the four 64-blocks' f16 d (a 32-block uses its 64-block's: half-block b -> scale b / 2)
 // (the GGUF fields of Q6_K are ql[128] | qh[64] | scales[16] | d, 210 bytes per superblock; prepared: 212)
@@ -40,7 +45,8 @@ namespace qm {
 
 enum : int {
   T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ2_XXS = 16, T_IQ2_XS = 17, T_IQ3_XXS = 18,
-  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_Q2_K = 10, T_Q3_K = 11, T_Q2_0 = 42
+  T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ2_S = 22, T_IQ4_XS = 23, T_Q2_K = 10, T_Q3_K = 11, T_Q2_0 = 42,
+  T_IQ1_S = 19, T_IQ1_M = 29
 };
 
 template <int TYPE> struct Traits;
@@ -61,6 +67,8 @@ template <> struct Traits<T_IQ2_S> { static constexpr int QB = 8, HB = 20, GGUF_
 template <> struct Traits<T_IQ3_XXS> { static constexpr int QB = 12, HB = 4, GGUF_SB = 98; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
 template <> struct Traits<T_Q2_K> { static constexpr int QB = 8, HB = 20, GGUF_SB = 84; static constexpr bool MINS = true, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_Q3_K> { static constexpr int QB = 12, HB = 20, GGUF_SB = 110; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
+template <> struct Traits<T_IQ1_S> { static constexpr int QB = 8, HB = 4, GGUF_SB = 50; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
+template <> struct Traits<T_IQ1_M> { static constexpr int QB = 8, HB = 4, GGUF_SB = 56; static constexpr bool MINS = false, SC16 = false, SPLIT = true; };
 template <> struct Traits<T_Q2_0> { static constexpr int QB = 8, HB = 8, GGUF_SB = 72; static constexpr bool MINS = false, SC16 = false, SPLIT = false; };
 // f16 scales per 32-block in the header (Q8_0's layout; Q2_0: one per 64-block), no integer sub-scales
 template <int TYPE> constexpr bool kBlockScales = TYPE == T_Q8_0 || TYPE == T_Q4_0 || TYPE == T_IQ4_NL || TYPE == T_Q2_0;
@@ -72,6 +80,7 @@ template <int TYPE> constexpr bool kMin16 = TYPE == T_Q2_K;
 template <int TYPE> constexpr bool kNeedsBsum = Traits<TYPE>::MINS || Traits<TYPE>::SC16;
 // the codebook types whose tables live in LDS
 template <int TYPE> constexpr bool kIq2 = TYPE == T_IQ2_XXS || TYPE == T_IQ2_XS || TYPE == T_IQ2_S || TYPE == T_IQ3_XXS;
+template <int TYPE> constexpr bool kIq1 = TYPE == T_IQ1_S || TYPE == T_IQ1_M;
 
 // A prepared weight as the kernels see it.
 struct WView {
@@ -278,6 +287,46 @@ __device__ __forceinline__ void iq_group(const IqLds<TYPE>* t, uint32_t p0, uint
     const uint4 m = t->sgn[si];
     w0 = (g.x ^ m.x) + m.z;
     w1 = (g.y ^ m.y) + m.w;
+  }
+}
+
+// ---- IQ1_S / IQ1_M (src/quants.h:263-296): the grid (ggml's iq1s_grid, every byte -1, 0 or 1) and, in LDS, one
+// word per entry: byte i holds (grid byte i) + 1 in bits 0-1 and (grid byte 4 + i) + 1 in bits 2-3, so an entry's
+// two int8x4 words of 8 * grid + delta are two byte permutes of a 3-value table.
+static __device__ const uint64_t g_iq1s_grid[2048] = QM_IQ1S_GRID_INIT;
+struct Iq1Lds {
+  uint32_t grid[2048];
+};
+__device__ __forceinline__ void iq1_lds_fill(Iq1Lds* t) {
+  for (int i = threadIdx.x; i < 2048; i += blockDim.x) {
+    const uint64_t g = g_iq1s_grid[i];
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t c0 = (uint32_t)((int)(int8_t)(g >> (8 * b)) + 1), c1 = (uint32_t)((int)(int8_t)(g >> (8 * b + 32)) + 1);
+      w |= (c0 | (c1 << 2)) << (8 * b);
+    }
+    t->grid[i] = w;
+  }
+}
+// elements 8l..8l+7 of a 32-block (grid entry idx, delta sign neg) -> two int8x4 words
+__device__ __forceinline__ void iq1_group(const Iq1Lds* t, uint32_t idx, bool neg, uint32_t& w0, uint32_t& w1) {
+  const uint32_t e = t->grid[idx];
+  const uint32_t tab = neg ? 0x0007FFF7u : 0x000901F9u;  // {8 (g) + delta} for g + 1 = 0, 1, 2: {-9, -1, 7} / {-7, 1, 9}
+  w0 = __builtin_amdgcn_perm(0u, tab, e & 0x03030303u);
+  w1 = __builtin_amdgcn_perm(0u, tab, (e >> 2) & 0x03030303u);
+}
+// group l's grid index and delta sign from a prepared IQ1 payload word pair (q0: index low bytes, q1: qh and scales)
+template <int TYPE>
+__device__ __forceinline__ void iq1_index(uint32_t q0, uint32_t q1, int l, uint32_t& idx, bool& neg) {
+  const uint32_t lo = (q0 >> (8 * l)) & 0xFFu;
+  if constexpr (TYPE == T_IQ1_S) {
+    idx = lo | (((q1 >> (3 * l)) & 7u) << 8);
+    neg = (q1 & 0x8000u) != 0;
+  } else {  // IQ1_M: byte l / 2 of q1, nibble l % 2: 3 index bits, then the sign bit
+    const uint32_t nib = (q1 >> (4 * l)) & 0xFu;
+    idx = lo | ((nib & 7u) << 8);
+    neg = (nib & 8u) != 0;
   }
 }
 

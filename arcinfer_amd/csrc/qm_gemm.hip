@@ -101,6 +101,17 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
     const uint32_t hb = q.z >> (4 * hf);
 #pragma unroll
     for (int k = 0; k < 4; ++k) r[k] |= (int)(((hb >> k) & 0x01010101u) << 4);
+  } else if constexpr (kIq1<TYPE>) {
+    // (k-half hf: groups 2 hf and 2 hf + 1 of the block)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      uint32_t idx, w0, w1;
+      bool neg;
+      iq1_index<TYPE>(q.x, q.y, 2 * hf + g, idx, neg);
+      iq1_group(tab, idx, neg, w0, w1);
+      r[2 * g] = (int)w0;
+      r[2 * g + 1] = (int)w1;
+    }
   } else if constexpr (kIq2<TYPE>) {
     uint32_t w0, w1, w2, w3;
     iq_group<TYPE>(tab, q.x, q.y, q.z, 0u, 2 * hf, w0, w1);
@@ -129,12 +140,20 @@ __device__ __forceinline__ v4i b_operand(uint4 q, uint4 hdr, int b, int hf, cons
   return r;
 }
 
-// Per-block weight scales of one superblock from its header (IQ2_XXS, IQ3_XXS: and its blocks' payloads pay, whose
-// last word holds the 4-bit scale): dsc[b] = d * sc_b (Q8_0: the block's f16 scale), dmn[b] = dmin * mn_b (Q4_K),
+// Per-block weight scales of one superblock from its header (IQ2_XXS, IQ3_XXS, IQ1_S: and its blocks' payloads pay,
+// which hold the integer scale): dsc[b] = d * sc_b (Q8_0: the block's f16 scale), dmn[b] = dmin * mn_b (Q4_K),
 // isc[b] = the integer scale.
 template <int TYPE>
 __device__ __forceinline__ void sb_scales(uint4 h, const uint4* pay, float dsc[8], float dmn[8], int isc[8]) {
-  if constexpr (TYPE == T_IQ2_XXS || TYPE == T_IQ3_XXS) {
+  if constexpr (TYPE == T_IQ1_S) {  // (the scale in bits 12-14 of the payload's qh)
+    const float d = h2f(h.x) * 0.125f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      isc[b] = 2 * (int)((pay[b].y >> 12) & 7u) + 1;
+      dsc[b] = d * (float)isc[b];
+      dmn[b] = 0.0f;
+    }
+  } else if constexpr (TYPE == T_IQ2_XXS || TYPE == T_IQ3_XXS) {
     const float d = h2f(h.x) * kIqDScale<TYPE>;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -341,7 +360,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   // (gate and up over two slot tiles: a ring of four blocks, two block pairs ahead, for the registers; the types whose
   //  block scales sit in the payloads need the whole superblock at its start)
   constexpr int NP = GU && MT == 2 ? 4 : 8;
-  static_assert(NP == 8 || (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS), "payload-held scales need the whole superblock");
+  static_assert(NP == 8 || (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS && TYPE != T_IQ1_S),
+                "payload-held scales need the whole superblock");
   uint4 pay[NP], pay2[GU ? NP : 1];
   uint4 hdr, hdr2 = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
@@ -680,6 +700,9 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
     } else if constexpr (TYPE == T_Q2_K) {  // (d and dmin first, then the 16 scale / min bytes)
       sc = make_uint4(h[1], h[2], h[3], h[4]);
       dd = h[0];
+    } else if constexpr (TYPE == T_IQ1_M) {  // (d alone: the scales are in the payloads)
+      sc = make_uint4(0u, 0u, 0u, 0u);
+      dd = h[0];
     } else {
       sc = make_uint4(h[0], h[1], h[2], h[3]);
       dd = h[4];
@@ -734,6 +757,16 @@ __global__ __launch_bounds__(256, 2) void gemm_s16_kernel(GemmArgs a) {
         for (int k = 0; k < 4; ++k) w[k] = ((w[k] | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
         sc0 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1))) & 0xFFu);
         sc1 = (int)(int8_t)((scw[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu);
+      } else if constexpr (TYPE == T_IQ1_M) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {  // (groups hf and 2 + hf: elements 8 hf .. 8 hf + 7 of each 16-element half)
+          uint32_t idx;
+          bool neg;
+          iq1_index<TYPE>(nib[b].x, nib[b].y, hf + 2 * g, idx, neg);
+          iq1_group(&L.tab, idx, neg, w[2 * g], w[2 * g + 1]);
+        }
+        sc0 = 2 * (int)((nib[b].y >> 16) & 7u) + 1;
+        sc1 = 2 * (int)((nib[b].y >> 19) & 7u) + 1;
       } else if constexpr (TYPE == T_Q3_K) {
         w[0] = q3_word(nib[b].x, nib[b].y, hw[b].x, 2 * hf);
         w[1] = q3_word(nib[b].x, nib[b].y, hw[b].x, 2 * hf + 1);
@@ -1000,7 +1033,8 @@ static hipError_t dispatch(int mode, const GemmArgs& a, hipStream_t s) {
     case GEMM_MOE_GATEUP:
       // (two slot tiles per work-group, each decoded weight operand feeding both; IQ2_XXS / IQ3_XXS keep their block
       //  scales in the payloads, which the two-tile kernel's payload ring does not hold whole)
-      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS) return go<TYPE, 2, GEMM_MOE_GATEUP, false>(a, s);
+      if constexpr (TYPE != T_IQ2_XXS && TYPE != T_IQ3_XXS && TYPE != T_IQ1_S)
+        return go<TYPE, 2, GEMM_MOE_GATEUP, false>(a, s);
       return go<TYPE, 1, GEMM_MOE_GATEUP, false>(a, s);
     case GEMM_MOE_DOWN:
       // (expert width F <= 512: the whole row's operands fit in registers; types with mins are not MoE types)
@@ -1042,6 +1076,7 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
     case T_Q6_K: return dispatch_s16<T_Q6_K>(mode, a, s);
     case T_Q3_K: return dispatch_s16<T_Q3_K>(mode, a, s);
     case T_Q2_K: return mode == GEMM_DENSE ? dispatch_s16<T_Q2_K>(mode, a, s) : hipErrorInvalidValue;
+    case T_IQ1_M: return mode == GEMM_DENSE ? dispatch_s16<T_IQ1_M>(mode, a, s) : hipErrorInvalidValue;
     case T_IQ2_XS: return dispatch_s16<T_IQ2_XS>(mode, a, s);
     case T_IQ2_S: return dispatch_s16<T_IQ2_S>(mode, a, s);
     default: break;
@@ -1057,6 +1092,7 @@ hipError_t launch_gemm(int type, int mode, const GemmArgs& a, hipStream_t s) {
     case T_Q5_K: return mode == GEMM_DENSE ? dispatch<T_Q5_K>(mode, a, s) : hipErrorInvalidValue;
     case T_IQ2_XXS: return dispatch<T_IQ2_XXS>(mode, a, s);
     case T_IQ3_XXS: return dispatch<T_IQ3_XXS>(mode, a, s);
+    case T_IQ1_S: return mode == GEMM_DENSE ? dispatch<T_IQ1_S>(mode, a, s) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

@@ -22,6 +22,8 @@ hipError_t launch_gemv(int type, const GemvArgs& a, hipStream_t s) {
     case T_Q3_K: return gemv_dispatch<T_Q3_K>(a, s);
     case T_Q2_0: return gemv_dispatch<T_Q2_0>(a, s);
     case T_Q2_K: return gemv_dispatch<T_Q2_K>(a, s);
+    case T_IQ1_S: return gemv_dispatch<T_IQ1_S>(a, s);
+    case T_IQ1_M: return gemv_dispatch<T_IQ1_M>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -18,7 +18,7 @@ namespace qm {
 template <int TYPE, int LPR, int R, int TB, int U, bool DUMP>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ typename LdsFor<TYPE>::type lds;
-  if constexpr (TYPE == T_IQ3_S || kIq2<TYPE>) {
+  if constexpr (TYPE == T_IQ3_S || kIq2<TYPE> || kIq1<TYPE>) {
     lds_fill<TYPE>(&lds);
     __syncthreads();
   }
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
 // more than 4 for Q6_K) or where two 4-token launches measured faster (IQ2_XXS at 4+ blocks per lane, applied to the
 // grid-decoded types alike); more tokens run as chunks.
 template <int TYPE>
-constexpr int gemvs_max_tb(int ch) { return ch <= (TYPE == T_Q6_K ? 4 : kIq2<TYPE> ? 3 : 5) ? 8 : 4; }
+constexpr int gemvs_max_tb(int ch) { return ch <= (TYPE == T_Q6_K ? 4 : (kIq2<TYPE> || kIq1<TYPE>) ? 3 : 5) ? 8 : 4; }
 
 // LDS bytes of gemvs_kernel for TB tokens (the per-16 sums for the types that read them: kNeedsBsum)
 template <int TYPE>
@@ -392,7 +392,7 @@ static hipError_t gos_tb(const GemvArgs& a, hipStream_t s) {
   }
 }
 
-template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S || kIq2<TYPE> ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
+template <int TYPE, int LPR, int R, int TB, bool DUMP, int U = (TYPE == T_IQ3_S || kIq2<TYPE> || kIq1<TYPE> ? 1 : TB == 1 ? 4 : TB <= 2 ? 2 : 1)>
 static hipError_t go(const GemvArgs& a, hipStream_t s) {
   constexpr int rows_per_wg = 4 * (64 / LPR) * R;
   const dim3 grid((unsigned)((a.w.rows + rows_per_wg - 1) / rows_per_wg)), block(256);

@@ -103,6 +103,39 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         }
       }
     }
+  } else if constexpr (TYPE == T_IQ1_S) {
+    // d | qs[32] | qh[8] (u16 per 32-block) (src/quants.h:263-276; decode.cl:326-345): block ib's payload = its 4 grid
+    // index low bytes and its qh
+    for (int ib = 0; ib < 8; ++ib) {
+      for (int e = 0; e < 4; ++e) q[8 * ib + e] = p[2 + 4 * ib + e];
+      q[8 * ib + 4] = p[34 + 2 * ib];
+      q[8 * ib + 5] = p[34 + 2 * ib + 1];
+      q[8 * ib + 6] = 0;
+      q[8 * ib + 7] = 0;
+    }
+    h[0] = p[0];
+    h[1] = p[1];
+    h[2] = 0;
+    h[3] = 0;
+  } else if constexpr (TYPE == T_IQ1_M) {
+    // qs[32] | qh[16] | scales (4 u16) (src/quants.h:277-296; decode.cl:346-366): block ib's payload = its 4 grid index
+    // low bytes, qh[2 ib], qh[2 ib + 1] and its two 3-bit scales (bits 6 (ib % 2) .. + 5 of scale word ib / 2); the
+    // f16 d is the top nibbles of the four scale words
+    const uint8_t *qs = p, *qh = p + 32, *sw = p + 48;
+    uint32_t w4[4];
+    for (int i = 0; i < 4; ++i) w4[i] = (uint32_t)sw[2 * i] | ((uint32_t)sw[2 * i + 1] << 8);
+    for (int ib = 0; ib < 8; ++ib) {
+      for (int e = 0; e < 4; ++e) q[8 * ib + e] = qs[4 * ib + e];
+      q[8 * ib + 4] = qh[2 * ib];
+      q[8 * ib + 5] = qh[2 * ib + 1];
+      q[8 * ib + 6] = (uint8_t)((w4[ib >> 1] >> (6 * (ib & 1))) & 0x3Fu);
+      q[8 * ib + 7] = 0;
+    }
+    const uint32_t su = (w4[0] >> 12) | ((w4[1] >> 8) & 0x00F0u) | ((w4[2] >> 4) & 0x0F00u) | (w4[3] & 0xF000u);
+    h[0] = (uint8_t)(su & 0xFF);
+    h[1] = (uint8_t)(su >> 8);
+    h[2] = 0;
+    h[3] = 0;
   } else if constexpr (TYPE == T_Q2_K) {
     // scales[16] (scale low nibble, min high nibble, per 16) | qs[64] | d | dmin (src/quants.h:159-169; decode.cl:151-160):
     // element e of 32-block ib has the value (qs[32 (ib / 4) + e] >> 2 (ib % 4)) & 3
@@ -232,6 +265,8 @@ hipError_t launch_repack(int type, const uint8_t* raw, int rows, int K, int kraw
     case T_Q6_K: repack_kernel<T_Q6_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q3_K: repack_kernel<T_Q3_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q2_K: repack_kernel<T_Q2_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ1_S: repack_kernel<T_IQ1_S><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
+    case T_IQ1_M: repack_kernel<T_IQ1_M><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q2_0: repack_kernel<T_Q2_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q5_K: repack_kernel<T_Q5_K><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;
     case T_Q4_0: repack_kernel<T_Q4_0><<<grid, block, 0, s>>>(raw, rows, K, kraw, qs, hdr); break;

@@ -2,7 +2,7 @@
 
 Geometry: src/gguf.h:43-72 of the reference (Q8_0 32 elements / 34 bytes, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144,
 Q5_K 256 / 176, Q6_K 256 / 210, IQ2_XXS 256 / 66, IQ2_XS 256 / 74, IQ2_S 256 / 82, IQ3_XXS 256 / 98, IQ3_S 256 / 110,
-IQ4_XS 256 / 136, Q2_K 256 / 84, Q3_K 256 / 110, and the reference's own Q2_0 64 / 18, src/gguf.h:26, 69). The synthetic generators produce the BASELINE configurations' distributions directly as block
+IQ4_XS 256 / 136, Q2_K 256 / 84, IQ1_S 256 / 50, IQ1_M 256 / 56, Q3_K 256 / 110, and the reference's own Q2_0 64 / 18, src/gguf.h:26, 69). The synthetic generators produce the BASELINE configurations' distributions directly as block
 bytes: every quant / index / sign / sub-scale bit uniform, the f16 super-scales |N(0, sigma)|.
 """
 import numpy as np
@@ -10,14 +10,15 @@ import numpy as np
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS = 2, 8, 12, 13, 14, 20, 21, 23
 IQ2_XXS, IQ2_XS, IQ3_XXS, IQ2_S = 16, 17, 18, 22
 Q2_K, Q3_K, Q2_0 = 10, 11, 42
+IQ1_S, IQ1_M = 19, 29
 TYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S",
               IQ4_XS: "IQ4_XS", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ3_XXS: "IQ3_XXS", IQ2_S: "IQ2_S", Q3_K: "Q3_K",
-              Q2_0: "Q2_0", Q2_K: "Q2_K"}
+              Q2_0: "Q2_0", Q2_K: "Q2_K", IQ1_S: "IQ1_S", IQ1_M: "IQ1_M"}
 TYPES_BY_NAME = {v: k for k, v in TYPE_NAMES.items()}
 
 # bytes of one 256-element superblock (Q8_0: 8 blocks of 34)
 SB_BYTES = {Q4_0: 144, Q8_0: 272, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 144, IQ3_S: 110, IQ4_XS: 136, IQ2_XXS: 66,
-            IQ2_XS: 74, IQ3_XXS: 98, IQ2_S: 82, Q3_K: 110, Q2_0: 72, Q2_K: 84}
+            IQ2_XS: 74, IQ3_XXS: 98, IQ2_S: 82, Q3_K: 110, Q2_0: 72, Q2_K: 84, IQ1_S: 50, IQ1_M: 56}
 
 
 SMALL_BLOCK_TYPES = (Q8_0, Q4_0, IQ4_NL, Q2_0)  # 32- (Q2_0: 64-) element blocks: rows may end inside a superblock
@@ -74,6 +75,8 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     Q3_K:   2-bit values, high bits and 6-bit scales uniform, d = f16(|N(0, 0.01)|) (d is the last field)
     Q2_0:   2-bit codes uniform, d = f16(|N(0, 0.02)|) per 64
     Q2_K:   2-bit values, 4-bit scales and mins uniform, d and dmin = f16(|N(0, 0.01)|) (the last two fields)
+    IQ1_S / IQ1_M: 11-bit grid indices, delta signs and 3-bit scales uniform, d = f16(|N(0, 0.01)|) (IQ1_M: its
+            bits in the top nibbles of the four scale words)
     """
     rng = np.random.default_rng(seed)
     nsb = K // 256
@@ -109,6 +112,13 @@ def synth_weight(qtype, N, K, seed, sigma=None):
     at = {Q6_K: 208, Q3_K: 108, Q2_K: 80}.get(qtype, 0)
     raw[:, at] = d & 0xFF
     raw[:, at + 1] = d >> 8
+    if qtype == IQ1_M:  # (d's 16 bits go to the top nibbles of the scale words at bytes 48..55)
+        sw = raw[:, 48:56].copy().view(np.uint16).reshape(-1, 4) & np.uint16(0x0FFF)
+        for i in range(4):
+            sw[:, i] |= ((d >> (4 * i)) & 0xF).astype(np.uint16) << 12
+        raw[:, 48:56] = sw.reshape(-1, 4).view(np.uint8).reshape(-1, 8)
+        raw[:, 0] = rng.integers(0, 256, N * nsb, dtype=np.uint8)  # (byte 0 is a grid index, not d)
+        raw[:, 1] = rng.integers(0, 256, N * nsb, dtype=np.uint8)
     if qtype in (Q4_K, Q5_K, Q2_K):
         dm = f16_bits(np.abs(rng.normal(0.0, sig, N * nsb)))
         am = 82 if qtype == Q2_K else 2

@@ -44,7 +44,7 @@ extern "C" {
 typedef enum {
   QM_Q4_0 = 2, QM_Q8_0 = 8, QM_Q4_K = 12, QM_Q5_K = 13, QM_Q6_K = 14, QM_IQ2_XXS = 16, QM_IQ2_XS = 17,
   QM_IQ3_XXS = 18, QM_IQ4_NL = 20, QM_IQ3_S = 21, QM_IQ2_S = 22, QM_IQ4_XS = 23, QM_Q2_K = 10, QM_Q3_K = 11,
-  QM_Q2_0 = 42
+  QM_IQ1_S = 19, QM_IQ1_M = 29, QM_Q2_0 = 42
 } qm_type;
 
 typedef enum {
@@ -71,7 +71,8 @@ const char* qmatmul_last_error(void);
 size_t qmatmul_sb_bytes(int type);
 
 /* Device bytes a prepared weight of `rows` x K takes (the GGUF bytes, plus 2 bytes of padding per IQ3_S, Q6_K,
- * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock and 6 per Q3_K superblock; a padded Q8_0 / Q4_0 / IQ4_NL / Q2_0
+ * IQ2_XXS, IQ2_XS, IQ2_S or IQ3_XXS superblock, 6 per Q3_K, 18 per IQ1_S and 12 per IQ1_M superblock; a padded
+ * Q8_0 / Q4_0 / IQ4_NL / Q2_0
  * row counts its zero blocks). */
 size_t qmatmul_weight_bytes(int type, int rows, int K);
 

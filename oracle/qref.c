@@ -19,6 +19,7 @@ static const uint64_t k_iq2xs_grid[512] = QM_IQ2XS_GRID_INIT;
 static const uint64_t k_iq2s_grid[1024] = QM_IQ2S_GRID_INIT;
 static const uint32_t k_iq3xxs_grid[256] = QM_IQ3XXS_GRID_INIT;
 static const uint8_t k_ksigns[128] = QM_KSIGNS_IQ2XS_INIT;
+static const uint64_t k_iq1s_grid[2048] = QM_IQ1S_GRID_INIT;
 
 /* src/quants.h:17-31 -- IEEE half to float, subnormals normalised by shifting */
 float qref_fp16_to_f32(uint16_t h) {
@@ -85,6 +86,8 @@ int qref_block_info(int type, int* blk, int* bytes) {
     case QREF_IQ3_XXS: *blk = 256; *bytes = 98; return 0;
     case QREF_Q3_K: *blk = 256; *bytes = 110; return 0;
     case QREF_Q2_K: *blk = 256; *bytes = 84; return 0;
+    case QREF_IQ1_S: *blk = 256; *bytes = 50; return 0;
+    case QREF_IQ1_M: *blk = 256; *bytes = 56; return 0;
     case QREF_Q2_0: *blk = 64; *bytes = 18; return 0;  /* (the reference's own type, src/gguf.h:26, 69) */
     default: return -1;
   }
@@ -169,6 +172,44 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
         o->d8[2 * g] = o->d8[2 * g + 1] = qref_fp16_to_f32(rd16(blk));
         o->sc[2 * g] = o->sc[2 * g + 1] = 1;
         for (int j = 0; j < 64; ++j) o->q[64 * g + j] = (int16_t)(((blk[2 + j / 4] >> (2 * (j % 4))) & 3) - 1);
+      }
+      return 0;
+    }
+    case QREF_IQ1_S: {
+      /* src/quants.h:263-276: d | qs[32] | qh[8] (u16 per 32: 3 high grid-index bits per 8 elements, bits 12-14 the
+       * scale, bit 15 the delta sign); wd = d / 8, sc = 2 s + 1, q = 8 * grid byte + delta */
+      const uint8_t* qs = p + 2;
+      o->d = qref_fp16_to_f32(rd16(p)) / 8;
+      for (int ib = 0; ib < 8; ++ib) {
+        const unsigned qh = rd16(p + 34 + 2 * ib);
+        o->sc[ib] = (int)(2 * ((qh >> 12) & 7) + 1);
+        const int dl = (qh & 0x8000) ? -1 : 1;
+        for (int l = 0; l < 4; ++l) {
+          const uint64_t g = k_iq1s_grid[qs[4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)];
+          for (int j = 0; j < 8; ++j) o->q[32 * ib + 8 * l + j] = (int16_t)(8 * (int)(int8_t)(g >> (8 * j)) + dl);
+        }
+      }
+      return 0;
+    }
+    case QREF_IQ1_M: {
+      /* src/quants.h:277-296: qs[32] | qh[16] | scales (4 u16: two 3-bit scales per 32-block, the f16 d in their top
+       * nibbles); per 8 elements 3 high grid-index bits and a delta sign in a nibble of qh */
+      const uint8_t *qs = p, *qh = p + 32;
+      const unsigned sc[4] = {rd16(p + 48), rd16(p + 50), rd16(p + 52), rd16(p + 54)};
+      const unsigned su = (sc[0] >> 12) | ((sc[1] >> 8) & 0x00f0) | ((sc[2] >> 4) & 0x0f00) | (sc[3] & 0xf000);
+      o->d = qref_fp16_to_f32((uint16_t)su) / 8;
+      for (int ib = 0; ib < 8; ++ib) {
+        o->sc16[2 * ib] = (int)(2 * ((sc[ib / 2] >> (6 * (ib % 2))) & 7) + 1);
+        o->sc16[2 * ib + 1] = (int)(2 * ((sc[ib / 2] >> (6 * (ib % 2) + 3)) & 7) + 1);
+        o->sc[ib] = o->sc16[2 * ib];
+        const unsigned h0 = qh[2 * ib], h1 = qh[2 * ib + 1];
+        const unsigned idx[4] = {qs[4 * ib] | ((h0 << 8) & 0x700), qs[4 * ib + 1] | ((h0 << 4) & 0x700),
+                                 qs[4 * ib + 2] | ((h1 << 8) & 0x700), qs[4 * ib + 3] | ((h1 << 4) & 0x700)};
+        const int dl[4] = {(h0 & 0x08) ? -1 : 1, (h0 & 0x80) ? -1 : 1, (h1 & 0x08) ? -1 : 1, (h1 & 0x80) ? -1 : 1};
+        for (int l = 0; l < 4; ++l) {
+          const uint64_t g = k_iq1s_grid[idx[l]];
+          for (int j = 0; j < 8; ++j) o->q[32 * ib + 8 * l + j] = (int16_t)(8 * (int)(int8_t)(g >> (8 * j)) + dl[l]);
+        }
       }
       return 0;
     }
@@ -353,7 +394,8 @@ static int decode_sb_raw(int type, const uint8_t* p, qref_sb* o) {
 
 int qref_decode_sb(int type, const uint8_t* p, qref_sb* o) {
   const int r = decode_sb_raw(type, p, o);
-  if (r == 0 && type != QREF_Q6_K && type != QREF_Q3_K && type != QREF_Q2_K && type != QREF_IQ2_XS && type != QREF_IQ2_S)
+  if (r == 0 && type != QREF_Q6_K && type != QREF_Q3_K && type != QREF_Q2_K && type != QREF_IQ2_XS && type != QREF_IQ2_S &&
+      type != QREF_IQ1_M)
     for (int i = 0; i < 16; ++i) o->sc16[i] = o->sc[i / 2];
   if (r == 0 && type != QREF_Q2_K)
     for (int i = 0; i < 16; ++i) o->mn16[i] = o->mn[i / 2];

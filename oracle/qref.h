@@ -20,7 +20,7 @@ extern "C" {
 /* GGML type ids (src/gguf.h:20-27) */
 enum { QREF_Q4_0 = 2, QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q5_K = 13, QREF_Q6_K = 14, QREF_IQ2_XXS = 16,
        QREF_IQ2_XS = 17, QREF_IQ3_XXS = 18, QREF_IQ4_NL = 20, QREF_IQ3_S = 21, QREF_IQ2_S = 22, QREF_IQ4_XS = 23,
-       QREF_Q2_K = 10, QREF_Q3_K = 11, QREF_Q2_0 = 42 };
+       QREF_Q2_K = 10, QREF_Q3_K = 11, QREF_IQ1_S = 19, QREF_IQ1_M = 29, QREF_Q2_0 = 42 };
 
 /* A decoded 256-element superblock: integer quants plus the per-type scales.
  *   Q8_0:   w[e] = d8[e/32] * q[e]
@@ -37,8 +37,10 @@ enum { QREF_Q4_0 = 2, QREF_Q8_0 = 8, QREF_Q4_K = 12, QREF_Q5_K = 13, QREF_Q6_K =
  *   Q3_K:   w[e] = d * sc16[e/16] * q[e]  (sc16 = 6-bit scale - 32 per 16, q = 2-bit value - (hmask bit ? 0 : 4))
  *   Q2_0:   w[e] = d8[e/32] * q[e]        (blocks of 64: one f16 d, q = 2-bit code - 1; d8 of both halves = d)
  *   Q2_K:   w[e] = d * sc16[e/16] * q[e] - dmin * mn16[e/16]   (q = 2-bit value, 4-bit scale and min per 16)
+ *   IQ1_S, IQ1_M: w[e] = d * sc16[e/16] * q[e]  (d = f16 d / 8, sc = 2 s + 1 per 32 (S) or per 16 (M), q = 8 * grid
+ *           byte + delta, delta = -1 / +1 per 32 (S) or per 8 (M))
  * sc16[i] is the integer scale of elements 16i..16i+15 for every type (sc16[2b] = sc16[2b+1] = sc[b] except Q6_K,
- * Q3_K, Q2_K, IQ2_XS and IQ2_S, whose scales are per 16); mn16[i] likewise the min of elements 16i..16i+15
+ * Q3_K, Q2_K, IQ2_XS, IQ2_S and IQ1_M, whose scales are per 16); mn16[i] likewise the min of elements 16i..16i+15
  * (= mn[i/2] but for Q2_K, whose mins are per 16). */
 typedef struct {
   float d, dmin;

@@ -200,3 +200,35 @@ def enc_q2_k(d, dmin, sc4, mn4, q):
         n, j, l = e // 128, (e % 128) // 32, e % 32
         qs[32 * n + l] |= int(q[e]) << (2 * j)
     return np.concatenate([scales, qs, _h(d), _h(dmin)])
+
+
+# ---- IQ1_S / IQ1_M (ggml-common.h block_iq1_s {d; qs[32]; qh[8] as u16}, block_iq1_m {qs[32]; qh[16]; scales[8]})
+def enc_iq1_s(d, s3, neg, gidx):
+    """s3: 8 scales 0..7 (sc = 2 s + 1), neg: 8 delta signs (per 32), gidx: 32 grid indices 0..2047 (4 per block, one
+    per 8 elements) -> 50 bytes: qh[ib] = 3 high index bits per group (bits 3l..3l+2) | s << 12 | neg << 15."""
+    qs = np.array([g & 0xFF for g in gidx], dtype=np.uint8)
+    qh = np.zeros(8, dtype=np.uint16)
+    for ib in range(8):
+        v = (int(s3[ib]) << 12) | (int(neg[ib]) << 15)
+        for l in range(4):
+            v |= ((int(gidx[4 * ib + l]) >> 8) & 7) << (3 * l)
+        qh[ib] = v
+    return np.concatenate([_h(d), qs, qh.view(np.uint8)])
+
+
+def enc_iq1_m(d, s3, neg, gidx):
+    """s3: 16 scales 0..7 (per 16), neg: 32 delta signs (per 8), gidx: 32 grid indices -> 56 bytes: qh per 8-group a
+    nibble (3 high index bits, sign bit 3), scales as 4 u16 of four 3-bit fields (bits 0-11) with d's 16 bits in their
+    top nibbles (word i holds d's bits 4i..4i+3)."""
+    qs = np.array([g & 0xFF for g in gidx], dtype=np.uint8)
+    qh = np.zeros(16, dtype=np.uint8)
+    for g in range(32):
+        qh[g // 2] |= ((((int(gidx[g]) >> 8) & 7) | (int(neg[g]) << 3)) << (4 * (g % 2)))
+    dbits = int(_h(d).view(np.uint16)[0])
+    sw = np.zeros(4, dtype=np.uint16)
+    for i in range(4):
+        v = 0
+        for f in range(4):
+            v |= int(s3[4 * i + f]) << (3 * f)
+        sw[i] = v | (((dbits >> (4 * i)) & 0xF) << 12)
+    return np.concatenate([qs, qh, sw.view(np.uint8)])

@@ -70,7 +70,8 @@ def test_producers_per256(qm, dev, M, Ms, K):
     _same_acts(got, oracle.quantize_act(xn, M_stride=Ms, act32=False))
 
 
-@pytest.mark.parametrize("qtype", [F.Q4_K, F.Q8_0, F.IQ4_XS, F.Q6_K, F.IQ3_S, F.Q5_K, F.Q3_K, F.Q2_0, F.Q2_K])
+@pytest.mark.parametrize("qtype", [F.Q4_K, F.Q8_0, F.IQ4_XS, F.Q6_K, F.IQ3_S, F.Q5_K, F.Q3_K, F.Q2_0, F.Q2_K, F.IQ1_S,
+                                   F.IQ1_M])
 @pytest.mark.parametrize("M,Ms,N,K", [(40, 48, 256, 2048), (256, 256, 384, 5120), (130, 130, 128, 1024)])
 def test_gemm_per256_parity(qm, dev, qtype, M, Ms, N, K):
     """Q4_K at M >= 128 runs the f16 kernel, everything else the int8 kernels: both read scale b >> 3."""

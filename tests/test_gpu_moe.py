@@ -335,7 +335,7 @@ def test_moe_refuses_min_types_and_checks_the_gate_column(qm, dev):
     import torch
     NE, E, Fd, T, NU = 8, 256, 256, 2, 2
     s = _moe_setup(qm, dev, NE, E, Fd, T, NU, F.IQ4_XS, seed=1)
-    for tk in (F.Q4_K, F.Q2_K):  # (per-block mins: no expert type, as the reference's)
+    for tk in (F.Q4_K, F.Q2_K, F.IQ1_S):  # (per-block mins, IQ1: no expert types, as the reference's)
         Wk = F.synth_weight(tk, NE * Fd, E, seed=2)
         wk = qm.QWeight(tk, to_dev(Wk, dev), NE * Fd, E)
         with pytest.raises(qm.QMatmulError) as ei:

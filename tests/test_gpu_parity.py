@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 TOL_INT8_PATH = 1e-4
 TOL_F32_REF = 1e-3
 TYPES = [F.Q8_0, F.Q4_K, F.IQ4_XS, F.IQ3_S]
-GEMV_TYPES = TYPES + [F.Q6_K, F.Q5_K, F.Q4_0, F.IQ4_NL, F.IQ2_XXS, F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0, F.Q2_K]
+GEMV_TYPES = TYPES + [F.Q6_K, F.Q5_K, F.Q4_0, F.IQ4_NL, F.IQ2_XXS, F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0, F.Q2_K,
+                      F.IQ1_S, F.IQ1_M]
 
 
 def rel_err(got, ref):

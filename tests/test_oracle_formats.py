@@ -133,7 +133,8 @@ def test_iq3_s_decoder_round_trip():
 
 
 @pytest.mark.parametrize("qtype", [F.Q4_0, F.Q8_0, F.Q4_K, F.Q5_K, F.Q6_K, F.IQ4_NL, F.IQ4_XS, F.IQ3_S, F.IQ2_XXS,
-                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0])
+                                   F.IQ2_XS, F.IQ2_S, F.IQ3_XXS, F.Q3_K, F.Q2_0, F.Q2_K,
+                                   F.IQ1_S, F.IQ1_M])
 def test_synth_weights_have_the_requested_statistics(qtype):
     W = F.synth_weight(qtype, 64, 512, seed=5)
     assert W.shape == (64, F.row_bytes(qtype, 512))
@@ -365,3 +366,54 @@ def test_per16_mins_enter_the_block_dot():
     want = sum(float(np.float32(asc[b, 0]) * (np.float32(d) * np.float32(0) - np.float32(dmin) * np.float32(want_m[b])))
                for b in range(8))
     assert abs(float(C[0, 0]) - want) <= 1e-6 * max(1.0, abs(want))
+
+
+def _iq1_grid():
+    import re
+    txt = open(oracle.HERE + "/iq_tables.inc").read()
+    body = re.search(r"QM_IQ1S_GRID_INIT \{(.*?)\}", txt, re.S).group(1)
+    g = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{16})ull", body)], dtype=np.uint64)
+    return g.view(np.int8).reshape(2048, 8).astype(np.int64)
+
+
+def test_iq1_codebook_published_and_invariants():
+    g = _iq1_grid()
+    assert g.shape == (2048, 8)
+    assert set(np.unique(g)) <= {-1, 0, 1}
+    assert np.all(g[0] == -1) and list(g[1]) == [1, -1, -1, -1, -1, -1, -1, -1]  # published first entries
+    assert len({tuple(r) for r in g}) == 2048  # distinct
+
+
+@pytest.mark.parametrize("qtype", [F.IQ1_S, F.IQ1_M])
+def test_iq1_decoders_round_trip(qtype):
+    """IQ1_S / IQ1_M (src/quants.h:263-296) against ggml's block structs: q = 8 * grid + delta, sc = 2 s + 1 (per 32
+    for IQ1_S, per 16 for IQ1_M), d / 8; grid entry 0 (all -1) with delta +1 gives -7 throughout."""
+    g = _iq1_grid()
+    rng = np.random.default_rng(qtype)
+    for it in range(25):
+        d = np.float16(abs(rng.standard_normal()) + 0.01)
+        gidx = rng.integers(0, 2048, 32)
+        if qtype == F.IQ1_S:
+            s3, neg = rng.integers(0, 8, 8), rng.integers(0, 2, 8)
+            if it == 0:
+                gidx[:], neg[:], s3[:] = 0, 0, 7
+            raw = enc.enc_iq1_s(d, s3, neg, gidx)
+            dl = np.repeat(np.where(neg == 1, -1, 1), 32)
+            sc16 = np.repeat(2 * s3 + 1, 2)
+        else:
+            s3, neg = rng.integers(0, 8, 16), rng.integers(0, 2, 32)
+            if it == 0:
+                gidx[:], neg[:], s3[:] = 0, 0, 7
+            raw = enc.enc_iq1_m(d, s3, neg, gidx)
+            dl = np.repeat(np.where(neg == 1, -1, 1), 8)
+            sc16 = 2 * s3 + 1
+        assert raw.size == F.SB_BYTES[qtype]
+        o = oracle.decode_sb(qtype, raw)
+        q = 8 * g[gidx].reshape(-1) + dl
+        assert np.array_equal(o["q"], q) and np.array_equal(o["sc16"], sc16)
+        assert o["d"] == np.float32(np.float32(d) / 8)
+        if it == 0:
+            assert np.all(o["q"] == -7)
+        w = oracle.dequant_rows(qtype, raw[None], 256)[0]
+        ref = (np.float32(np.float32(d) / 8) * sc16[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32))
+        assert np.array_equal(w, ref.astype(np.float32))
