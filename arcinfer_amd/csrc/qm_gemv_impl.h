@@ -108,9 +108,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // Batch-1 decode GEMV, persistent sweep. LPR lanes share a row (32, or 128 = two waves with an LDS combine); lane j
 // takes blocks j, j + LPR, ... (CH of them). The grid is a few work-groups per CU and lane group g walks rows
 // g, g + G, g + 2G, ... (G = lane groups in the grid), so the whole grid moves through the weight matrix together
-// and every group has one row in flight: it decodes the row once its loads land and only then issues the next row's
-// loads. Measured on MI355X this beats issuing every row's loads up front (the decode then piles up behind the
-// stream). The token's int8 row, its per-32 scales (and Q4_K / Q5_K / Q6_K per-16 sums) are staged in LDS once per
+// and every group has at most two rows in flight (batch 1; one with several tokens): row i + 1's loads are issued
+// before row i is decoded. Measured on MI355X this beats issuing every row's loads up front (the decode then piles up
+// behind the stream) and a third row in flight. The token's int8 row, its per-32 scales (and Q4_K / Q5_K / Q6_K per-16 sums) are staged in LDS once per
 // work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
 // consecutive blocks read consecutive 16-byte words. DUMP: the same kernel writes each block's int32 sums
 // (dbg_isum, and Q4_K / Q5_K min sums to dbg_msum) instead of the output.
@@ -151,7 +151,14 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   };
   // (with several waves per row every group of the work-group runs its first group's step count, for the combine's
   // barrier; the extra steps of its other groups recompute a row past the end without storing it)
-  const int steps = WPR == 1 ? steps_of(g0) : steps_of((int)blockIdx.x * GPW);
+  // (two rows in flight, no split: the first group of a wave has the most rows, and every group of the wave runs its
+  //  step count -- a group's extra step reads a clamped row and stores nothing. A wave-uniform trip count keeps the
+  //  loop off the exec mask; with a per-group count the compiler must assume the loads of a step that some lanes
+  //  skipped are still pending at the next fetch, and waits there for nearly every load in flight. Measured on the
+  //  IQ4_XS gate/up shape: 10.86 -> 10.53 us; the multi-token launches keep the per-group count, 17.9 -> 17.8 us at T 4)
+  const int steps = WPR > 1 ? steps_of((int)blockIdx.x * GPW)
+                    : (SPLIT || PF != 2) ? steps_of(g0)
+                            : __builtin_amdgcn_readfirstlane(steps_of((int)blockIdx.x * GPW + (int)(threadIdx.x / 64) * (64 / LPR)));
   RawBlk cur[CH];
   auto fetch = [&](int i, RawBlk* dst) {
     const int n = min(row_of(i), rows - 1);
@@ -273,6 +280,13 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
       // every token from LDS up front and runs out of registers)
       if constexpr (TB >= 8) __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (PF == 2 && !EXACT) {
+      // (the last chunk is decoded under a branch that whole waves skip; a use of its registers on every path marks
+      //  its loads complete here -- otherwise the compiler assumes them pending at the next fetch and waits there for
+      //  nearly every load in flight, the other row's included)
+#pragma unroll
+      for (int u = 0; u < CH; ++u) asm volatile("" ::"v"(cur[u].q0), "v"(cur[u].h));
+    }
     if constexpr (WPR > 1) {
       // each wave's row sum goes to LDS; every RC rows one barrier, then lane j of the group adds the WPR partials of
       // the chunk's row j (in wave order) and stores it. Two chunk buffers: a chunk's partials are read after the
@@ -318,14 +332,18 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   if constexpr (PF == 2) {
     // two rows in flight per group: row i + 1's loads are issued before row i is decoded (two register sets that
     // alternate, so no copy waits for a load)
+    // (no exit between the two halves: with one, the compiler merges the path that leaves after the first half into
+    //  the loop head, takes that half's loads as pending there and waits for nearly every load in flight before the
+    //  next fetch)
     RawBlk nxt[CH];
-    for (int i = 0; i < steps; i += 2) {
+    int i = 0;
+    for (; i + 1 < steps; i += 2) {
       fetch(i + 1, nxt);  // (clamped to the last row: loads past the group's rows are harmless)
       row_step(i, cur);
-      if (i + 1 >= steps) break;
       fetch(i + 2, cur);
       row_step(i + 1, nxt);
     }
+    if (i < steps) row_step(i, cur);
   } else {
     for (int i = 0; i < steps; ++i) {
       row_step(i, cur);
@@ -351,8 +369,8 @@ template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = 
           bool SPLIT = false>
 static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
-  // batch 1: two rows in flight per lane group (three measured slower: 11.7 -> 13.0 us on the down projection,
-  // 10.7 -> 12.3 on gate/up); more tokens: registers to tokens
+  // batch 1: two rows in flight per lane group (three measured slower: 11.4 -> 13.0 us on the down projection,
+  // 10.5 -> 11.8 on gate/up, also with one work-group per CU); more tokens: registers to tokens
   constexpr int PF = TB == 1 ? 2 : 1;
   // Persistent grid: PC work-groups per CU (two; three with four waves per row or where measured faster), or as many
   // as the kernel's registers and LDS let reside (the 8-token instantiation needs more than 256 registers: one wave per
