@@ -105,6 +105,19 @@ def timed_graph(fn, args, stream):
     return ms / args.steps
 
 
+def timed_graph_n(fn, n, stream):
+    """fn(0..n-1) captured once and replayed (a warm-up replay, the settle time, then one timed replay); ms per call."""
+    import torch
+    for i in range(2):
+        fn(i)
+    torch.cuda.synchronize()
+    g = graphed(fn, n)
+    if SETTLE_S > 0:
+        settle(g.replay)
+    ms, _ = timed(lambda i: g.replay(), 1, 0, stream, pre=g.replay)
+    return ms / n
+
+
 def profile_traffic(kernel_key):
     """Bytes per launch from the committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, calibrated on a copy
     kernel), or None."""
@@ -388,8 +401,9 @@ def main():
                      ("add_norm_quant", lambda i: qm.add_norm_quant(x, t, wv, 1e-6, 1.0),
                       M * 12 * K + 4 * K + M * outb(K)))
             for nm, fn, byts in cases:
-                msp = timed_graph(fn, args, stream) if M == 1 else timed(fn, max(2, args.steps // 5), args.warmup,
-                                                                           stream)[0]
+                # (both sizes as graph replays: an eager launch through the Python wrapper costs tens of microseconds of
+                #  host time, more than the 2048-row kernels themselves; 20 launches per graph at 2048 rows)
+                msp = timed_graph(fn, args, stream) if M == 1 else timed_graph_n(fn, 20, stream)
                 prod[f"{nm}_M{M}"] = {"us": round(msp * 1e3, 2), "GB/s": round(byts / (msp * 1e-3) / 1e9, 1)}
         rep["producers_K5120_F17408"] = prod
         out["reported"] = rep
