@@ -65,3 +65,21 @@ def test_argument_errors_need_no_gpu(qm):
     assert lib.qmatmul_swiglu_quant_ex(buf, 576, 288, 1, 1, 0, 0, 0, buf, buf, buf, None) == 2
     with pytest.raises(qm.QMatmulError):
         qm._call("qmatmul_moe_ws_layout", 0, 1, 1, 1, 1, None)
+
+
+def test_type_table_agrees_across_header_binding_and_library(qm):
+    """Every qm_type of the header has the GGML id the Python formats use, and the library reports the GGUF bytes per
+    256 elements the formats module (and ggml's block structs) give it."""
+    from arcinfer_amd import formats as F
+    txt = open(os.path.join(ROOT, "include", "qmatmul.h")).read()
+    ids = {k: int(v) for k, v in re.findall(r"\bQM_((?:I?Q)\w+?)\s*=\s*(\d+)", txt)}
+    assert len(ids) == 17
+    lib = qm.load_library()
+    for name, tid in ids.items():
+        assert getattr(F, name) == tid, name
+        assert lib.qmatmul_sb_bytes(tid) == F.SB_BYTES[tid], name
+    # rows: whole superblocks, except the 32-element block types (any K % 32 == 0, padded) and Q2_0 (K % 64 == 0)
+    for tid in ids.values():
+        ok640 = lib.qmatmul_weight_bytes(tid, 16, 640) > 0
+        assert ok640 == (tid in (F.Q8_0, F.Q4_0, F.IQ4_NL, F.Q2_0)), tid
+    assert lib.qmatmul_weight_bytes(F.Q2_0, 16, 608) == 0 and lib.qmatmul_weight_bytes(F.Q8_0, 16, 608) > 0
