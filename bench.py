@@ -406,6 +406,28 @@ def main():
                 msp = timed_graph(fn, args, stream) if M == 1 else timed_graph_n(fn, 20, stream)
                 prod[f"{nm}_M{M}"] = {"us": round(msp * 1e3, 2), "GB/s": round(byts / (msp * 1e-3) / 1e9, 1)}
         rep["producers_K5120_F17408"] = prod
+        if not args.profile:
+            # every weight type at the gate/up shape (K 5120 -> N 17408, batch 1), rotated over more than 256 MB
+            K, N = 5120, 17408
+            x = torch.from_numpy(F.synth_activations(1, K, seed=70)).to(dev)
+            aq, asc, absum = qm.quantize_act(x, M_stride=16)
+            C = torch.empty((1, N), device=dev)
+            types = {}
+            for qtype in sorted(F.TYPE_NAMES):
+                Wd = torch.from_numpy(F.synth_weight(qtype, N, K, seed=71)).to(dev)
+                b = F.weight_bytes(qtype, N, K)
+                ncopy = max(2, -(-300_000_000 // b))
+                copies = [qm.QWeight(qtype, Wd, N, K) for _ in range(ncopy)]
+                del Wd
+                msg = timed_graph(lambda i, copies=copies: qm.gemv(copies[i % len(copies)], aq, asc, absum, C=C, ldc=N),
+                                  args, stream)
+                types[F.TYPE_NAMES[qtype]] = {"us_per_launch": round(msg * 1e3, 2),
+                                              "weight_GB/s": round(b / (msg * 1e-3) / 1e9, 1),
+                                              "frac_of_hbm_peak": round(b / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                              "copies": ncopy}
+                for c in copies:
+                    c.release()
+            rep["gemv_types_5120x17408"] = types
         out["reported"] = rep
         torch.cuda.empty_cache()
 
