@@ -81,7 +81,8 @@ def test_quantizer_strided_input(qm, dev):
 @pytest.mark.parametrize("N,K,T", [(64, 1024, 1), (48, 768, 3), (40, 8192, 1), (16, 256, 8),
                                    (24, 17408, 1), (20, 17408, 2),   # 128 lanes per row (two waves combined)
                                    (32, 6144, 8), (40, 4096, 6),     # tokens chunked per launch
-                                   (16, 34816, 1), (12, 33024, 3)])  # K > 32768: the generic kernel
+                                   (16, 34816, 1), (12, 33024, 3),   # K > 32768: the generic kernel
+                                   (6160, 5120, 1)])  # 32 lanes per row, 5 blocks per lane (batch-1 per-type routes)
 def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
     rng = np.random.default_rng(qtype + N + K)
     W = F.synth_weight(qtype, N, K, seed=qtype * 7 + K)
@@ -101,7 +102,8 @@ def test_gemv_blocksums_bit_exact(qm, dev, qtype, N, K, T):
                                    (64, 34816, 1), (24, 33024, 3),  # (K > 32768: the generic kernel)
                                    # tokens per launch capped at 4 (6 blocks per lane; Q6_K beyond 4, the IQ2 grids
                                    # beyond 3): 8 tokens as two launches, 6 as 4 + 2
-                                   (48, 6144, 8), (32, 5120, 8), (40, 4096, 6)])
+                                   (48, 6144, 8), (32, 5120, 8), (40, 4096, 6),
+                                   (6160, 5120, 1)])  # (more than 6144 rows: the 32-lane batch-1 route)
 def test_gemv_f32_parity(qm, dev, qtype, N, K, T):
     import torch
     rng = np.random.default_rng(qtype * 3 + N)
