@@ -108,3 +108,21 @@ def test_gguf_to_gemv(qm, dev, tmp_path):
     ref = oracle.blockdot(F.IQ4_XS, W1, 512, aq.cpu().numpy(), asc.cpu().numpy(), absum.cpu().numpy(), M=1)
     assert np.max(np.abs(y.cpu().numpy() - ref)) <= 1e-4 * np.max(np.abs(ref))
     w.release()
+
+
+def test_gguf_every_weight_type_sized_by_its_block(qm, tmp_path):
+    """A tensor of each of the 17 weight types: the reader sizes it from ggml's block geometry (elements and bytes per
+    block, Q2_0 the reference's 64 / 18) and hands back the bytes written."""
+    tens, ws = [], {}
+    for i, qtype in enumerate(sorted(F.TYPE_NAMES)):
+        W = F.synth_weight(qtype, 3, 512, seed=90 + i)
+        ws[qtype] = W
+        tens.append((f"t.{F.TYPE_NAMES[qtype]}", qtype, [512, 3], W.tobytes()))
+    p = os.path.join(str(tmp_path), "types.gguf")
+    gw.write_gguf(p, [("general.architecture", gw.STR, "x")], tens)
+    with qm.GgufFile(p) as g:
+        assert len(g) == 17
+        for qtype, W in ws.items():
+            t = g.tensor(f"t.{F.TYPE_NAMES[qtype]}")
+            assert (t.qtype, t.K, t.rows, t.nbytes) == (qtype, 512, 3, W.nbytes), F.TYPE_NAMES[qtype]
+            assert t.nbytes == 3 * F.row_bytes(qtype, 512) and np.array_equal(t.numpy(), W.ravel())
