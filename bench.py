@@ -136,7 +136,7 @@ def main():
     global SETTLE_S
     SETTLE_S = 0.0 if args.profile else args.settle_ms / 1e3
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the multi-GPU design is "
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sharding across GPUs is "
               "designed but not built: every box here has one GPU)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
