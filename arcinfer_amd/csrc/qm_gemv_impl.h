@@ -370,8 +370,10 @@ template <int TYPE, int LPR, int CH, bool EXACT, int TB, bool DUMP, bool AREG = 
 static hipError_t gos(const GemvArgs& a0, hipStream_t s) {
   constexpr int GPW = 256 / LPR;
   // batch 1: two rows in flight per lane group (three measured slower: 11.4 -> 13.0 us on the down projection,
-  // 10.5 -> 11.8 on gate/up, also with one work-group per CU); more tokens: registers to tokens
-  constexpr int PF = TB == 1 ? 2 : 1;
+  // 10.5 -> 11.8 on gate/up, also with one work-group per CU); two tokens: two rows as well where the registers
+  // allow (IQ4_XS 5120 -> 17408 at T 2: 13.7 -> 12.6 us); more tokens: registers to tokens (at T 4 two rows spill:
+  // 17.7 -> 21.6 us)
+  constexpr int PF = TB == 1 || (TB == 2 && CH <= 5) ? 2 : 1;
   // Persistent grid: PC work-groups per CU (two; three with four waves per row or where measured faster), or as many
   // as the kernel's registers and LDS let reside (the 8-token instantiation needs more than 256 registers: one wave per
   // SIMD), so the whole grid is resident at once; fewer when the matrix has fewer rows than lane groups. Occupancy is
