@@ -108,10 +108,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // Batch-1 decode GEMV, persistent sweep. LPR lanes share a row (32, or 128 = two waves with an LDS combine); lane j
 // takes blocks j, j + LPR, ... (CH of them). The grid is a few work-groups per CU and lane group g walks rows
 // g, g + G, g + 2G, ... (G = lane groups in the grid), so the whole grid moves through the weight matrix together
-// and every group has at most two rows in flight (batch 1; one with several tokens): row i + 1's loads are issued
-// before row i is decoded. Measured on MI355X this beats issuing every row's loads up front (the decode then piles up
-// behind the stream) and a third row in flight. The token's int8 row, its per-32 scales (and Q4_K / Q5_K / Q6_K per-16 sums) are staged in LDS once per
-// work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
+// and every group has at most two rows in flight (one or two tokens; one row with more): row i + 1's loads are
+// issued before row i is decoded. Measured on MI355X this beats issuing every row's loads up front (the decode then
+// piles up behind the stream) and a third row in flight. The token's int8 row, its per-32 scales (and Q4_K / Q5_K /
+// Q6_K per-16 sums) are staged in LDS once per work-group; the int8 row is split into two planes (bytes 0-15 and 16-31 of each 32-block) so lanes reading
 // consecutive blocks read consecutive 16-byte words. DUMP: the same kernel writes each block's int32 sums
 // (dbg_isum, and Q4_K / Q5_K min sums to dbg_msum) instead of the output.
 //
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(NT) void gemvs_kernel(GemvArgs a) {
   //  step count -- a group's extra step reads a clamped row and stores nothing. A wave-uniform trip count keeps the
   //  loop off the exec mask; with a per-group count the compiler must assume the loads of a step that some lanes
   //  skipped are still pending at the next fetch, and waits there for nearly every load in flight. Measured on the
-  //  IQ4_XS gate/up shape: 10.86 -> 10.53 us; the multi-token launches keep the per-group count, 17.9 -> 17.8 us at T 4)
+  //  IQ4_XS gate/up shape: 10.86 -> 10.53 us; the one-row-in-flight launches keep the per-group count)
   const int steps = WPR > 1 ? steps_of((int)blockIdx.x * GPW)
                     : (SPLIT || PF != 2) ? steps_of(g0)
                             : __builtin_amdgcn_readfirstlane(steps_of((int)blockIdx.x * GPW + (int)(threadIdx.x / 64) * (64 / LPR)));
